@@ -1,0 +1,161 @@
+/*
+ * qma_gpu.h -- C-ABI of the MI355X (gfx950) quantized MoE expert-matmul
+ * library (libqmagpu.so).
+ *
+ * Two groups of entry points:
+ *
+ * 1. Reference-compatible: the exact names and signatures the qma engine
+ *    binds from src/q8k.c (declared at src/qma.h:358-365).  Host pointers,
+ *    caller-owned buffers, no status returns, unknown wtype -> 0.0f.  They
+ *    run on the GPU (staged per calling thread) so a build that drops
+ *    src/q8k.c and links this library keeps working unchanged; they are
+ *    per-row calls and therefore latency-bound.  qma_q8k_available() reports
+ *    whether a usable gfx950 device is present.
+ *
+ * 2. Device entries (qmag_*): the coarse seams of src/nn.c -- matmul
+ *    (nn.c:307) and moe_ffn (nn.c:509) -- over weights resident in HBM in the
+ *    GGUF block layout.  All pointers are device pointers, work is ordered on
+ *    the library stream, and each returns an int status (0 ok, <0 error;
+ *    qmag_last_error() gives the text).
+ *
+ * Weight formats: GGML Q4_K (type 12, 144-byte super-blocks) and Q6_K
+ * (type 14, 210-byte super-blocks), src/qma.h:67-90.  Activation Q8_K is the
+ * planar form of src/q8k.c:32-85: xq int8[n], xd f32[n/256], xsum i16[n/16].
+ */
+#ifndef QMA_GPU_H
+#define QMA_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QMAG_TYPE_Q4_K 12
+#define QMAG_TYPE_Q6_K 14
+
+#define QMAG_OK 0
+#define QMAG_ERR_HIP (-1)      /* a HIP runtime call failed                  */
+#define QMAG_ERR_ARG (-2)      /* unsupported shape / type / null pointer    */
+#define QMAG_ERR_NODEV (-3)    /* no gfx950 device, or qmag_init not called  */
+#define QMAG_ERR_KERNEL (-4)   /* a kernel reported an internal guard trip   */
+
+/* ------------------------------------------------------------------------ */
+/* Reference-compatible entries                                              */
+/* ------------------------------------------------------------------------ */
+
+/* replaces qma_q8k_available, src/q8k.c:271-278 (qma.h:359) */
+int qma_q8k_available(void);
+
+/* replaces qma_q8k_quant, src/q8k.c:280-288 (qma.h:360) */
+void qma_q8k_quant(const float *x, int n, int8_t *xq, float *xd, int16_t *xsum);
+
+/* replaces qma_q8k_dot, src/q8k.c:305-316 (qma.h:361-362) */
+float qma_q8k_dot(const void *row, int wtype, const int8_t *xq, const float *xd,
+                  const int16_t *xsum, int n);
+
+/* replaces qma_q8k_gateup, src/q8k.c:291-302 (qma.h:364-365) */
+void qma_q8k_gateup(const void *g, const void *u, const int8_t *xq, const float *xd,
+                    const int16_t *xsum, int n, float *gate, float *up);
+
+/* ------------------------------------------------------------------------ */
+/* Runtime                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Select device `device`, create the library stream.  Idempotent. */
+int qmag_init(int device);
+const char *qmag_last_error(void);
+/* CU count, clock (kHz), HBM bytes, gfx arch name (>= 16 chars buffer). */
+int qmag_device_info(int *n_cu, int *clock_khz, size_t *hbm_bytes, char *arch, int arch_len);
+
+int qmag_malloc(void **dptr, size_t bytes);
+int qmag_free(void *dptr);
+int qmag_h2d(void *dst, const void *src, size_t bytes);      /* synchronous */
+int qmag_d2h(void *dst, const void *src, size_t bytes);      /* synchronous */
+int qmag_d2d(void *dst, const void *src, size_t bytes);      /* stream-ordered */
+int qmag_memset(void *dst, int value, size_t bytes);         /* stream-ordered */
+int qmag_sync(void);
+
+/* Timing on the library stream: record event `slot` (0..63) and read the
+   elapsed milliseconds between two recorded slots (synchronises on b). */
+int qmag_event_record(int slot);
+int qmag_event_elapsed(int a, int b, float *ms);
+
+/* Per-kernel timing (the QMA_TIMING role, nn.c:219-259, on the GPU): while
+   enabled, every kernel the MoE entries launch is bracketed by HIP events on
+   the library stream.  Kernel ids: 0 router, 1 top-k/Q8_K(x), 2 gate/up,
+   3 Q8_K(h), 4 down+combine, 5 fused decode.  qmag_prof_read synchronises and
+   returns the launch count and summed milliseconds of one id. */
+int qmag_prof_enable(int on);
+int qmag_prof_read(int kernel_id, long *count, double *total_ms);
+
+/* ------------------------------------------------------------------------ */
+/* Device entries                                                            */
+/* ------------------------------------------------------------------------ */
+
+/* Q8_K quantization of T rows of n floats (n % 256 == 0); q8k.c:34-85. */
+int qmag_q8k_quant_dev(const float *x, int n, int T, int8_t *xq, float *xd, int16_t *xsum);
+
+/* out[t][r] = row_r(W) . Q8_K(x[t]) for pre-quantised activations;
+   mm_worker, nn.c:276-289.  n_in in {256,512,1024,2048,4096,8192}. */
+int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum,
+                        const void *W, int n_in, int n_out, int T, int wtype, float *out);
+
+/* matmul seam, nn.c:307-345: quantise each x[t] once, then the matvec. */
+int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
+                    float *out);
+
+/* One MoE FFN layer's tensors, resident in HBM (device pointers).  Field
+   meaning follows qma_t.layers[il] (src/qma.h:202-218); expert slabs are
+   expert-major as in the GGUF (src/gguf.c:268-271, nn.c:668-674). */
+typedef struct qmag_moe_layer {
+    int n_embd;                 /* 2048 */
+    int n_ff;                   /* 512  */
+    int n_expert;               /* 256  */
+    int n_used;                 /* 8    */
+    const float *gate_inp;      /* f32 [n_expert][n_embd] router (ffn_gate_inp)       */
+    const float *router_bias;   /* f32 [n_expert] or NULL: synthetic logit skew        */
+    const void *gate_exps;      /* Q4_K, n_expert x n_ff rows of n_embd               */
+    const void *up_exps;        /* Q4_K, same shape                                   */
+    const void *down_exps;      /* Q4_K/Q6_K, n_expert x n_embd rows of n_ff          */
+    int t_down_exps;
+    const float *gate_inp_shexp;/* f32 [n_embd] shared-expert gate                    */
+    const void *gate_shexp;     /* Q4_K, n_ff rows of n_embd                          */
+    const void *up_shexp;
+    const void *down_shexp;     /* Q4_K/Q6_K, n_embd rows of n_ff                     */
+    int t_down_shexp;
+} qmag_moe_layer;
+
+/* moe_ffn seam, nn.c:509-649: out[t] = sum_k w_k * expert_k(x[t]) +
+   sigmoid(gs) * shared(x[t]) for T tokens (x, out: f32 [T][n_embd]). */
+int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *out, int T);
+
+/* Decode over a stack of MoE layers: for each of n_tok tokens in turn,
+   x[t] <- x[t] + moe_l(x[t]) for l = 0..n_layer-1 (the residual add of
+   qma_eval, nn.c:2252).  x: f32 [n_tok][n_embd], updated in place. */
+int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, float *x, int n_tok);
+
+/* Stage outputs of the last qmag_moe_ffn_dev / qmag_moe_stack_dev layer for
+   token 0 (device pointers the library owns, valid until the next call):
+   logits f32[n_expert], sel i32[n_used], w f32[n_used], gs f32[1],
+   h f32[(n_used+1)][n_ff] (slot n_used = shared expert). */
+int qmag_moe_last_stage(const float **logits, const int **sel, const float **w,
+                        const float **gs, const float **h);
+
+/* ------------------------------------------------------------------------ */
+/* Synthetic inputs (bench/test utilities; not part of the reference)        */
+/* ------------------------------------------------------------------------ */
+
+/* f32 ~ N(mean, std) from a counter-based generator keyed by seed. */
+int qmag_synth_normal(uint64_t seed, size_t n, float mean, float std, float *out);
+/* N(0, std) weights generated and quantised to Q4_K / Q6_K in one pass
+   (n % 256 == 0); same quantiser as qmag_quantize_dev. */
+int qmag_synth_weights(uint64_t seed, size_t n, float std, int wtype, void *out);
+/* fp32 -> Q4_K / Q6_K with the build's quantiser (n % 256 == 0). */
+int qmag_quantize_dev(const float *x, size_t n, int wtype, void *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,332 @@
+// qmag_device.h -- device-side building blocks for gfx950 (wave64, CDNA4).
+//
+// GGUF super-block layouts (src/qma.h:77-90), fp16 decode, DPP/permlane
+// wave reductions, and the per-lane dot "tasks" the matvec and MoE kernels
+// are built from.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QK_K 256
+#define Q4K_BYTES 144
+#define Q6K_BYTES 210
+
+namespace qmag {
+
+// ---------------------------------------------------------------- fp16 ----
+__device__ __forceinline__ float h2f(uint32_t h16)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+// ------------------------------------------------------------ reductions --
+// All-reduce over aligned groups of W lanes (W = 4, 8, 16, 32, 64) using DPP
+// quad permutes, row mirrors and the gfx950 permlane swaps; no LDS traffic.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <- 7-i within 8
+constexpr int DPP_MIRROR = 0x140;      // lane i <- 15-i within 16
+
+template <int W>
+__device__ __forceinline__ float group_sum(float v)
+{
+    if constexpr (W >= 2) v += dpp_f<DPP_XOR1>(v);
+    if constexpr (W >= 4) v += dpp_f<DPP_XOR2>(v);
+    if constexpr (W >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
+    if constexpr (W >= 16) v += dpp_f<DPP_MIRROR>(v);
+    if constexpr (W >= 32) {
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    if constexpr (W >= 64) {
+        auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ int group_sum_i(int v)
+{
+    if constexpr (W >= 2) v += dpp_i<DPP_XOR1>(v);
+    if constexpr (W >= 4) v += dpp_i<DPP_XOR2>(v);
+    if constexpr (W >= 8) v += dpp_i<DPP_HALF_MIRROR>(v);
+    if constexpr (W >= 16) v += dpp_i<DPP_MIRROR>(v);
+    if constexpr (W >= 32) {
+        auto p = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = (int)(p[0] + p[1]);
+    }
+    if constexpr (W >= 64) {
+        auto p = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = (int)(p[0] + p[1]);
+    }
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ float group_max(float v)
+{
+    if constexpr (W >= 2) v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    if constexpr (W >= 4) v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    if constexpr (W >= 8) v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    if constexpr (W >= 16) v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    if constexpr (W >= 32) {
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    }
+    if constexpr (W >= 64) {
+        auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    }
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ float group_min(float v)
+{
+    if constexpr (W >= 2) v = fminf(v, dpp_f<DPP_XOR1>(v));
+    if constexpr (W >= 4) v = fminf(v, dpp_f<DPP_XOR2>(v));
+    if constexpr (W >= 8) v = fminf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    if constexpr (W >= 16) v = fminf(v, dpp_f<DPP_MIRROR>(v));
+    if constexpr (W >= 32) {
+        auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fminf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    }
+    if constexpr (W >= 64) {
+        auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fminf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    }
+    return v;
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+// --------------------------------------------------------------- loads ----
+// Byte-addressed loads.  Q6_K super-blocks are 210 B, so odd blocks sit at
+// 2-byte alignment; gfx9 global memory runs in unaligned mode and these
+// compile to single global_load_dword{,x2,x4}.
+__device__ __forceinline__ uint4 ld16(const uint8_t *p)
+{
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t *p)
+{
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p)
+{
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld2(const uint8_t *p)
+{
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
+{
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// -------------------------------------------------------------- Q8_K -----
+// One wave quantises one 256-float block (src/q8k.c:34-85).  Lane l holds
+// elements 4l..4l+3.  Outputs: the 4 int8 packed in a word, the block scale
+// d, and in every lane the 16-element group sum of its group (lanes 4k..4k+3
+// share group k).  amax is an exact max; d = amax/127 and 1/d are IEEE
+// divisions; q = clamp(round-half-away(x * inv), +-127).
+struct Q8Lane {
+    uint32_t packed;
+    float d;
+    int gsum;
+};
+
+__device__ __forceinline__ int q8_round(float v)
+{
+    int q = (int)__builtin_roundf(v);
+    q = q > 127 ? 127 : q;
+    q = q < -127 ? -127 : q;
+    return q;
+}
+
+__device__ __forceinline__ Q8Lane q8k_quant_lane(float4 v)
+{
+    float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    const float amax = group_max<64>(a);
+    Q8Lane r;
+    r.d = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / r.d;
+    const int q0 = q8_round(v.x * inv), q1 = q8_round(v.y * inv);
+    const int q2 = q8_round(v.z * inv), q3 = q8_round(v.w * inv);
+    r.packed = (uint32_t)(q0 & 255) | ((uint32_t)(q1 & 255) << 8) | ((uint32_t)(q2 & 255) << 16) |
+               ((uint32_t)(q3 & 255) << 24);
+    r.gsum = group_sum_i<4>(q0 + q1 + q2 + q3);
+    return r;
+}
+
+// -------------------------------------------------------------- Q4_K -----
+// Task = (super-block ib, 64-lane group g): bytes qs[32g..32g+31] give the
+// low nibbles of sub-block 2g and the high nibbles of sub-block 2g+1.
+// Plo/Phi are the exact 32-lane int32 sums of src/q8k.c:117-120.
+struct Q4Act {      // activation operand of one Q4_K task
+    uint32_t x[16]; // xq[256ib+64g .. +63]
+    float xd;       // xd[ib]
+    float sx0, sx1; // xsum pairs of sub-blocks 2g, 2g+1 as floats
+};
+
+__device__ __forceinline__ void q4_load_act(Q4Act &a, const int8_t *xq, const float *xd,
+                                            const int16_t *xsum, int ib, int g)
+{
+    const uint4 *p = (const uint4 *)(xq + ib * QK_K + 64 * g);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint4 w = p[k];
+        a.x[4 * k + 0] = w.x;
+        a.x[4 * k + 1] = w.y;
+        a.x[4 * k + 2] = w.z;
+        a.x[4 * k + 3] = w.w;
+    }
+    a.xd = xd[ib];
+    const uint2 s = *(const uint2 *)(xsum + ib * 16 + 4 * g);
+    const int s0 = (int16_t)(s.x & 0xffff), s1 = (int16_t)(s.x >> 16);
+    const int s2 = (int16_t)(s.y & 0xffff), s3 = (int16_t)(s.y >> 16);
+    a.sx0 = (float)(s0 + s1);
+    a.sx1 = (float)(s2 + s3);
+}
+
+// 6-bit (scale, min) of sub-block j (src/q8k.c:22-30) from the 12 scale
+// bytes held as words y = bytes 0-3, z = 4-7, w = 8-11.
+__device__ __forceinline__ void q4_scale_min(int j, uint32_t y, uint32_t z, uint32_t w,
+                                             uint32_t &sc, uint32_t &m)
+{
+    const int sh = 8 * (j & 3);
+    const uint32_t by = (y >> sh) & 255, bz = (z >> sh) & 255, bw = (w >> sh) & 255;
+    if (j < 4) {
+        sc = by & 63;
+        m = bz & 63;
+    } else {
+        sc = (bw & 15) | ((by >> 6) << 4);
+        m = (bw >> 4) | ((bz >> 6) << 4);
+    }
+}
+
+struct Q4Int {
+    int plo, phi;
+};
+
+__device__ __forceinline__ Q4Int q4_int_dot(uint4 q0, uint4 q1, const Q4Act &a)
+{
+    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    int lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        lo = sdot4(qw[k] & 0x0F0F0F0Fu, a.x[k], lo);
+        hi = sdot4((qw[k] >> 4) & 0x0F0F0F0Fu, a.x[8 + k], hi);
+    }
+    return {lo, hi};
+}
+
+// fp32 contribution of one task: (d*s1*xd)*Plo + (d*s2*xd)*Phi
+//                                 - (dmin*m1*sx0 + dmin*m2*sx1)*xd
+__device__ __forceinline__ float q4_task(uint4 hdr, uint4 q0, uint4 q1, const Q4Act &a, int g)
+{
+    const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
+    uint32_t s1, m1, s2, m2;
+    q4_scale_min(2 * g, hdr.y, hdr.z, hdr.w, s1, m1);
+    q4_scale_min(2 * g + 1, hdr.y, hdr.z, hdr.w, s2, m2);
+    const Q4Int p = q4_int_dot(q0, q1, a);
+    const float d1 = d * (float)s1, d2 = d * (float)s2;
+    const float mm1 = dmin * (float)m1, mm2 = dmin * (float)m2;
+    const float acc = (float)p.plo * (d1 * a.xd) + (float)p.phi * (d2 * a.xd);
+    const float bias = (mm1 * a.sx0 + mm2 * a.sx1) * a.xd;
+    return acc - bias;
+}
+
+// -------------------------------------------------------------- Q6_K -----
+// Task = (super-block ib, half n, lane-half l16): 16 lanes l = 16*l16+t of
+// half n across its four 32-lane quarters (src/quants.c:57-73,
+// src/q8k.c:225-257).  The four tasks of a block sit in one lane quad and
+// their int32 partials add to the exact per-block sum of q8k.c:259.
+struct Q6Act {
+    uint32_t x[16]; // quarter Q words 4Q..4Q+3: xq[256ib+128n+32Q+16l16 .. +15]
+};
+
+__device__ __forceinline__ void q6_load_act(Q6Act &a, const int8_t *xq, int ib, int n, int l16)
+{
+#pragma unroll
+    for (int Q = 0; Q < 4; Q++) {
+        const uint4 w = *(const uint4 *)(xq + ib * QK_K + 128 * n + 32 * Q + 16 * l16);
+        a.x[4 * Q + 0] = w.x;
+        a.x[4 * Q + 1] = w.y;
+        a.x[4 * Q + 2] = w.z;
+        a.x[4 * Q + 3] = w.w;
+    }
+}
+
+struct Q6Raw {      // the bytes of one Q6_K task
+    uint4 ql_lo, ql_hi, qh;
+    uint2 sc;       // scales[8n .. 8n+7]
+    uint32_t d;     // fp16 bits
+};
+
+__device__ __forceinline__ void q6_load_raw(Q6Raw &r, const uint8_t *blk, int n, int l16)
+{
+    r.ql_lo = ld16(blk + 64 * n + 16 * l16);
+    r.ql_hi = ld16(blk + 64 * n + 32 + 16 * l16);
+    r.qh = ld16(blk + 128 + 32 * n + 16 * l16);
+    r.sc = ld8(blk + 192 + 8 * n);
+    r.d = ld2(blk + 208);
+}
+
+// bytes (q6 - 32) for q6 in 0..63, per byte without cross-byte borrow
+__device__ __forceinline__ uint32_t q6_center(uint32_t q)
+{
+    return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ int q6_int_dot(const Q6Raw &r, const Q6Act &a, int l16)
+{
+    const uint32_t L[4] = {r.ql_lo.x, r.ql_lo.y, r.ql_lo.z, r.ql_lo.w};
+    const uint32_t H[4] = {r.ql_hi.x, r.ql_hi.y, r.ql_hi.z, r.ql_hi.w};
+    const uint32_t B[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    int s[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t w0 = (L[k] & 0x0F0F0F0Fu) | ((B[k] & 0x03030303u) << 4);
+        const uint32_t w1 = (H[k] & 0x0F0F0F0Fu) | (((B[k] >> 2) & 0x03030303u) << 4);
+        const uint32_t w2 = ((L[k] >> 4) & 0x0F0F0F0Fu) | (((B[k] >> 4) & 0x03030303u) << 4);
+        const uint32_t w3 = ((H[k] >> 4) & 0x0F0F0F0Fu) | (((B[k] >> 6) & 0x03030303u) << 4);
+        s[0] = sdot4(q6_center(w0), a.x[0 + k], s[0]);
+        s[1] = sdot4(q6_center(w1), a.x[4 + k], s[1]);
+        s[2] = sdot4(q6_center(w2), a.x[8 + k], s[2]);
+        s[3] = sdot4(q6_center(w3), a.x[12 + k], s[3]);
+    }
+    // scale of quarter Q is scales[8n + l16 + 2Q] = byte (l16 + 2Q) of r.sc
+    const uint64_t sc8 = ((uint64_t)r.sc.y << 32) | r.sc.x;
+    int tot = 0;
+#pragma unroll
+    for (int Q = 0; Q < 4; Q++) {
+        const int scq = (int)(int8_t)((sc8 >> (8 * (l16 + 2 * Q))) & 255);
+        tot += s[Q] * scq;
+    }
+    return tot;
+}
+
+}  // namespace qmag

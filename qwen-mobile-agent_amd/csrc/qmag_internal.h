@@ -1,0 +1,63 @@
+// qmag_internal.h -- host-side internals shared by the library's units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/qma_gpu.h"
+#include "qmag_device.h"
+
+namespace qmag {
+
+struct Ctx {
+    bool ready = false;
+    int dev = -1;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev[64] = {};
+    int n_cu = 0;
+    int clock_khz = 0;
+    size_t hbm = 0;
+    char arch[64] = {0};
+};
+
+Ctx &ctx();
+// status helpers: record a message for qmag_last_error() and return code
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char *what, const char *file, int line);
+int require_ready();
+
+#define QMAG_HIP(call)                                                        \
+    do {                                                                      \
+        hipError_t _e = (call);                                               \
+        if (_e != hipSuccess) return qmag::hip_fail(_e, #call, __FILE__, __LINE__); \
+    } while (0)
+
+// Grow-on-demand device workspace, one buffer per slot (never shrinks).
+enum WsSlot {
+    WS_XQ = 0, WS_XD, WS_XS,        // Q8_K of the layer input(s)
+    WS_LOGITS, WS_SEL, WS_W, WS_GS, // router outputs
+    WS_H, WS_HQ, WS_HD, WS_HS,      // expert hidden state and its Q8_K
+    WS_LAYERS,                      // device copy of layer descriptors
+    WS_OUT,                         // layer output scratch
+    WS_FLAGS,                       // kernel status / counters
+    WS_COUNT
+};
+void *workspace(int slot, size_t bytes, int *status);
+
+// ---- per-kernel event timing (qmag_prof_*) ----
+enum ProfId { PROF_ROUTER = 0, PROF_TOPK, PROF_GATEUP, PROF_HQUANT, PROF_DOWN, PROF_FUSED, PROF_COUNT };
+bool prof_on();
+void prof_begin(int id, hipStream_t s);
+void prof_end(int id, hipStream_t s);
+
+// ---- launchers (all stream-ordered on s) ----
+int launch_q8k_quant(const float *x, int nblocks, int8_t *xq, float *xd, int16_t *xsum,
+                     hipStream_t s);
+int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
+                  int n_in, int n_out, int T, int wtype, float *out, hipStream_t s);
+int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const float *resid,
+            hipStream_t s);
+int moe_check_layer(const qmag_moe_layer *L);
+
+}  // namespace qmag

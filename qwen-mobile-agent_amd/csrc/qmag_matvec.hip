@@ -1,0 +1,206 @@
+// qmag_matvec.hip -- Q8_K activation quantisation and the Q4_K / Q6_K x Q8_K
+// matvec (src/q8k.c:34-262 driven as in mm_worker, src/nn.c:276-289).
+//
+// Decode matvecs are HBM-bound: each row's bytes are read once.  A row is
+// split into "tasks" (Q4_K: one 64-lane group of a super-block = 32 B of
+// nibbles + the 16 B header; Q6_K: a quarter of a super-block = 3x16 B +
+// scales + d).  LPR lanes cooperate on a row (LPR = tasks per row, <= 64) so
+// a wave covers 64/LPR rows per step; each lane keeps its task's activation
+// slice in registers across rows and issues its weight loads for U row
+// steps before consuming any of them.  Row sums use DPP/permlane reductions.
+#include "qmag_internal.h"
+
+namespace qmag {
+
+__global__ __launch_bounds__(256) void q8k_quant_kernel(const float *__restrict__ x, int nblocks,
+                                                        int8_t *__restrict__ xq,
+                                                        float *__restrict__ xd,
+                                                        int16_t *__restrict__ xsum)
+{
+    const int blk = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    if (blk >= nblocks) return;           // wave-uniform
+    const int lane = lane_id();
+    const float4 v = ((const float4 *)(x + (size_t)blk * QK_K))[lane];
+    const Q8Lane r = q8k_quant_lane(v);
+    ((uint32_t *)(xq + (size_t)blk * QK_K))[lane] = r.packed;
+    if (lane == 0) xd[blk] = r.d;
+    if ((lane & 3) == 0) xsum[(size_t)blk * 16 + (lane >> 2)] = (int16_t)r.gsum;
+}
+
+int launch_q8k_quant(const float *x, int nblocks, int8_t *xq, float *xd, int16_t *xsum,
+                     hipStream_t s)
+{
+    if (nblocks <= 0) return QMAG_OK;
+    if (!x || !xq || !xd || !xsum) return fail(QMAG_ERR_ARG, "q8k_quant: null pointer");
+    const int wgs = (nblocks + 3) / 4;
+    hipLaunchKernelGGL(q8k_quant_kernel, dim3(wgs), dim3(256), 0, s, x, nblocks, xq, xd, xsum);
+    QMAG_HIP(hipGetLastError());
+    return QMAG_OK;
+}
+
+// ------------------------------------------------------------------------
+template <int WT>
+struct RowTask;
+
+template <>
+struct RowTask<QMAG_TYPE_Q4_K> {
+    struct Raw {
+        uint4 hdr, q0, q1;
+    };
+    using Act = Q4Act;
+    static constexpr int BLOCK = Q4K_BYTES;
+    __device__ static void load_raw(Raw &r, const uint8_t *blk, int q)
+    {
+        r.hdr = ld16(blk);
+        r.q0 = ld16(blk + 16 + 32 * q);
+        r.q1 = ld16(blk + 32 + 32 * q);
+    }
+    __device__ static void load_act(Act &a, const int8_t *xq, const float *xd, const int16_t *xs,
+                                    int ib, int q)
+    {
+        q4_load_act(a, xq, xd, xs, ib, q);
+    }
+    // float contribution of this lane's task
+    __device__ static float dot(const Raw &r, const Act &a, int q)
+    {
+        return q4_task(r.hdr, r.q0, r.q1, a, q);
+    }
+};
+
+template <>
+struct RowTask<QMAG_TYPE_Q6_K> {
+    using Raw = Q6Raw;
+    struct Act {
+        Q6Act a;
+        float xd;
+    };
+    static constexpr int BLOCK = Q6K_BYTES;
+    __device__ static void load_raw(Raw &r, const uint8_t *blk, int q)
+    {
+        q6_load_raw(r, blk, q >> 1, q & 1);
+    }
+    __device__ static void load_act(Act &a, const int8_t *xq, const float *xd, const int16_t *,
+                                    int ib, int q)
+    {
+        q6_load_act(a.a, xq, ib, q >> 1, q & 1);
+        a.xd = xd[ib];
+    }
+    // the quad's int32 block sum is formed exactly, then d*xd*isum once
+    __device__ static float dot(const Raw &r, const Act &a, int q)
+    {
+        const int part = q6_int_dot(r, a.a, q & 1);
+        const int isum = group_sum_i<4>(part);
+        return q == 0 ? h2f(r.d) * a.xd * (float)isum : 0.0f;
+    }
+};
+
+template <int WT, int NB, bool ONE_TOKEN>
+__global__ __launch_bounds__(256) void matvec_kernel(const uint8_t *__restrict__ W,
+                                                     const int8_t *__restrict__ xq,
+                                                     const float *__restrict__ xd,
+                                                     const int16_t *__restrict__ xsum,
+                                                     float *__restrict__ out, int n_out, int T)
+{
+    using RT = RowTask<WT>;
+    constexpr int TPR = 4 * NB;                 // tasks per row
+    constexpr int LPR = TPR < 64 ? TPR : 64;    // lanes per row
+    constexpr int TPL = TPR / LPR;              // tasks per lane
+    constexpr int RPW = 64 / LPR;               // rows per wave step
+    constexpr int U = 2;                        // wave steps in flight
+    constexpr size_t RB = (size_t)NB * RT::BLOCK;
+    constexpr int N_IN = NB * QK_K;
+
+    const int lane = lane_id();
+    const int sub = lane % LPR, rw = lane / LPR;
+    const int q = sub & 3;
+    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nwave = (int)((gridDim.x * blockDim.x) >> 6);
+
+    typename RT::Act act[TPL];
+    if constexpr (ONE_TOKEN) {
+#pragma unroll
+        for (int j = 0; j < TPL; j++) RT::load_act(act[j], xq, xd, xsum, (sub + LPR * j) >> 2, q);
+    }
+
+    for (int base = wave * RPW * U; base < n_out; base += nwave * RPW * U) {
+        typename RT::Raw raw[U][TPL];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int row = base + u * RPW + rw;
+#pragma unroll
+            for (int j = 0; j < TPL; j++) {
+                if (row < n_out)
+                    RT::load_raw(raw[u][j], W + (size_t)row * RB + (size_t)((sub + LPR * j) >> 2) * RT::BLOCK, q);
+                else
+                    raw[u][j] = typename RT::Raw{};
+            }
+        }
+        for (int t = 0; t < T; t++) {
+            if constexpr (!ONE_TOKEN) {
+#pragma unroll
+                for (int j = 0; j < TPL; j++)
+                    RT::load_act(act[j], xq + (size_t)t * N_IN, xd + (size_t)t * NB,
+                                 xsum + (size_t)t * (N_IN / 16), (sub + LPR * j) >> 2, q);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                float v = 0.0f;
+#pragma unroll
+                for (int j = 0; j < TPL; j++) v += RT::dot(raw[u][j], act[j], q);
+                v = group_sum<LPR>(v);
+                const int row = base + u * RPW + rw;
+                if (sub == 0 && row < n_out) out[(size_t)t * n_out + row] = v;
+            }
+        }
+    }
+}
+
+template <int WT, int NB>
+static int launch_mv_nb(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
+                        int n_out, int T, float *out, hipStream_t s)
+{
+    constexpr int TPR = 4 * NB;
+    constexpr int LPR = TPR < 64 ? TPR : 64;
+    constexpr int RPW = 64 / LPR;
+    const long groups = ((long)n_out + RPW * 2 - 1) / (RPW * 2);
+    const long cap = (long)(ctx().n_cu > 0 ? ctx().n_cu : 256) * 32;    // waves
+    const long waves = groups < cap ? groups : cap;
+    const int wgs = (int)((waves + 3) / 4);
+    if (T == 1)
+        hipLaunchKernelGGL((matvec_kernel<WT, NB, true>), dim3(wgs), dim3(256), 0, s,
+                           (const uint8_t *)W, xq, xd, xsum, out, n_out, T);
+    else
+        hipLaunchKernelGGL((matvec_kernel<WT, NB, false>), dim3(wgs), dim3(256), 0, s,
+                           (const uint8_t *)W, xq, xd, xsum, out, n_out, T);
+    QMAG_HIP(hipGetLastError());
+    return QMAG_OK;
+}
+
+template <int WT>
+static int launch_mv_t(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
+                       int n_in, int n_out, int T, float *out, hipStream_t s)
+{
+    switch (n_in / QK_K) {
+    case 1: return launch_mv_nb<WT, 1>(xq, xd, xsum, W, n_out, T, out, s);
+    case 2: return launch_mv_nb<WT, 2>(xq, xd, xsum, W, n_out, T, out, s);
+    case 4: return launch_mv_nb<WT, 4>(xq, xd, xsum, W, n_out, T, out, s);
+    case 8: return launch_mv_nb<WT, 8>(xq, xd, xsum, W, n_out, T, out, s);
+    case 16: return launch_mv_nb<WT, 16>(xq, xd, xsum, W, n_out, T, out, s);
+    case 32: return launch_mv_nb<WT, 32>(xq, xd, xsum, W, n_out, T, out, s);
+    default: return fail(QMAG_ERR_ARG, "matvec: n_in=%d not in {256..8192} powers of two", n_in);
+    }
+}
+
+int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W, int n_in,
+                  int n_out, int T, int wtype, float *out, hipStream_t s)
+{
+    if (n_in <= 0 || n_in % QK_K || n_out <= 0 || T <= 0)
+        return fail(QMAG_ERR_ARG, "matvec: n_in=%d n_out=%d T=%d", n_in, n_out, T);
+    if (!xq || !xd || !W || !out || (wtype == QMAG_TYPE_Q4_K && !xsum))
+        return fail(QMAG_ERR_ARG, "matvec: null pointer");
+    if (wtype == QMAG_TYPE_Q4_K) return launch_mv_t<QMAG_TYPE_Q4_K>(xq, xd, xsum, W, n_in, n_out, T, out, s);
+    if (wtype == QMAG_TYPE_Q6_K) return launch_mv_t<QMAG_TYPE_Q6_K>(xq, xd, xsum, W, n_in, n_out, T, out, s);
+    return fail(QMAG_ERR_ARG, "matvec: unsupported wtype %d", wtype);
+}
+
+}  // namespace qmag

@@ -1,0 +1,480 @@
+// qmag_moe.hip -- MoE FFN layer (src/nn.c:509-707, q8k branch) as a launch
+// sequence over HBM-resident experts:
+//
+//   router_kernel   logits[t][e] = Wr[e] . x[t] (+ synthetic bias)   nn.c:514-524
+//   topk_kernel     softmax, top-n_used (strict >, lowest index wins),
+//                   renormalised weights; Q8_K(x[t]); shared-expert gate
+//                   sigmoid(wsh . deq(Q8_K(x)))                       nn.c:525-536, 452-454, 598-602
+//   gateup_kernel   per (slot, row): g,u = two Q4_K rows . Q8_K(x), h = silu(g)*u
+//                   slot < n_used: routed expert sel[slot]; slot n_used: shared
+//                                                                     nn.c:423-432, 458-464
+//   q8k_quant       Q8_K(h) per slot                                  nn.c:434, 465
+//   down_kernel     out[r] = sum_k w_k * down_k[r] . Q8_K(h_k) + gs * down_sh[r] . Q8_K(h_sh)
+//                   in the reference's combine order (k = 0..n_used-1, then shared),
+//                   optionally plus a residual                         nn.c:435-437, 468-472, 614-629
+#include "qmag_internal.h"
+
+namespace qmag {
+
+// --------------------------------------------------------------- router --
+__global__ __launch_bounds__(256) void router_kernel(const float *__restrict__ Wr,
+                                                     const float *__restrict__ bias,
+                                                     const float *__restrict__ x, int N, int E,
+                                                     int T, float *__restrict__ logits)
+{
+    const int wid = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    if (wid >= E * T) return;
+    const int t = wid / E, e = wid % E;
+    const int lane = lane_id();
+    const float *w = Wr + (size_t)e * N;
+    const float *xp = x + (size_t)t * N;
+    float s = 0.0f;
+    for (int i = 4 * lane; i < N; i += 256) {
+        const float4 a = *(const float4 *)(w + i);
+        const float4 b = *(const float4 *)(xp + i);
+        s += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+    }
+    s = group_sum<64>(s);
+    if (lane == 0) logits[(size_t)t * E + e] = bias ? s + bias[e] : s;
+}
+
+// ----------------------------------------------------------------- top-k --
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m)
+{
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits,
+                                                   const float *__restrict__ x,
+                                                   const float *__restrict__ wsh, int N, int E,
+                                                   int K, int *__restrict__ sel,
+                                                   float *__restrict__ wout,
+                                                   float *__restrict__ gs_out,
+                                                   int8_t *__restrict__ xq, float *__restrict__ xd,
+                                                   int16_t *__restrict__ xs)
+{
+    __shared__ int8_t s_xq[4096];
+    __shared__ float s_xd[16];
+    __shared__ float s_red[4];
+    const int t = blockIdx.x;
+    const int lane = lane_id(), wv = threadIdx.x >> 6;
+    const int NB = N / QK_K;
+
+    // Q8_K of x[t]: one wave per 256-block
+    for (int b = wv; b < NB; b += 4) {
+        const float4 v = ((const float4 *)(x + (size_t)t * N + b * QK_K))[lane];
+        const Q8Lane r = q8k_quant_lane(v);
+        ((uint32_t *)(xq + (size_t)t * N + b * QK_K))[lane] = r.packed;
+        ((uint32_t *)(s_xq + b * QK_K))[lane] = r.packed;
+        if (lane == 0) {
+            xd[(size_t)t * NB + b] = r.d;
+            s_xd[b] = r.d;
+        }
+        if ((lane & 3) == 0) xs[(size_t)t * (N / 16) + b * 16 + (lane >> 2)] = (int16_t)r.gsum;
+    }
+
+    if (wv == 0) {
+        // softmax over E <= 256 logits, 4 per lane
+        const float *lg = logits + (size_t)t * E;
+        float l[4], p[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            l[j] = e < E ? lg[e] : -INFINITY;
+            mx = fmaxf(mx, l[j]);
+        }
+        mx = group_max<64>(mx);
+        float se = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            p[j] = e < E ? expf(l[j] - mx) : 0.0f;
+            se += p[j];
+        }
+        se = group_sum<64>(se);
+        unsigned long long key[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            p[j] = p[j] / se;
+            // p >= 0: its bit pattern orders like the value; ~e makes the
+            // lowest index win among equal probabilities
+            key[j] = e < E ? (((unsigned long long)__float_as_uint(p[j]) << 32) | (uint32_t)~e) : 0ull;
+        }
+        float wk[8];
+        int sk[8];
+        for (int k = 0; k < K; k++) {
+            unsigned long long b = key[0];
+#pragma unroll
+            for (int j = 1; j < 4; j++) b = key[j] > b ? key[j] : b;
+#pragma unroll
+            for (int m = 1; m < 64; m <<= 1) {
+                const unsigned long long o = shfl_xor_u64(b, m);
+                b = o > b ? o : b;
+            }
+            const int e = (int)~(uint32_t)b;
+            sk[k] = e;
+            wk[k] = __uint_as_float((uint32_t)(b >> 32));
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (lane + 64 * j == e) key[j] = 0ull;
+        }
+        if (lane == 0) {
+            float ws = 0.0f;
+            for (int k = 0; k < K; k++) ws += wk[k];
+            for (int k = 0; k < K; k++) {
+                sel[(size_t)t * K + k] = sk[k];
+                wout[(size_t)t * K + k] = wk[k] / ws;
+            }
+        }
+    }
+    __syncthreads();
+
+    // shared-expert gate: sum_i wsh[i] * xq[i] * xd[i/256], then sigmoid
+    float g = 0.0f;
+    for (int i = threadIdx.x; i < N; i += 256) g += wsh[i] * (float)s_xq[i] * s_xd[i / QK_K];
+    g = group_sum<64>(g);
+    if (lane == 0) s_red[wv] = g;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float s = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+        gs_out[t] = 1.0f / (1.0f + expf(-s));
+    }
+}
+
+// --------------------------------------------------------------- gate/up --
+// A wave holds R = 32/LPR row pairs: lanes [0,32) the gate rows, lanes
+// [32,64) the matching up rows.  After the per-row reduction the two halves
+// swap values with permlane32 so the gate lane sees its up value.
+template <int NBE>
+__global__ __launch_bounds__(256) void gateup_kernel(const uint8_t *__restrict__ gate_exps,
+                                                     const uint8_t *__restrict__ up_exps,
+                                                     const uint8_t *__restrict__ gate_sh,
+                                                     const uint8_t *__restrict__ up_sh,
+                                                     const int *__restrict__ sel, int K, int F,
+                                                     const int8_t *__restrict__ xq,
+                                                     const float *__restrict__ xd,
+                                                     const int16_t *__restrict__ xs,
+                                                     float *__restrict__ h)
+{
+    constexpr int TPR = 4 * NBE;
+    constexpr int LPR = TPR < 32 ? TPR : 32;
+    constexpr int TPL = TPR / LPR;
+    constexpr int R = 32 / LPR;              // row pairs per wave step
+    constexpr int U = 2;
+    constexpr size_t RB = (size_t)NBE * Q4K_BYTES;
+
+    const int lane = lane_id();
+    const int half = lane >> 5, l32 = lane & 31;
+    const int sub = l32 % LPR, rr = l32 / LPR, q = sub & 3;
+    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int steps_per_slot = (F + R * U - 1) / (R * U);
+    const int slot = wave / steps_per_slot;
+    if (slot > K) return;
+    const int base = (wave % steps_per_slot) * R * U;
+
+    const uint8_t *mat;
+    if (slot < K) {
+        const size_t slab = (size_t)F * RB;
+        mat = (half ? up_exps : gate_exps) + (size_t)sel[slot] * slab;
+    } else {
+        mat = half ? up_sh : gate_sh;
+    }
+
+    Q4Act act[TPL];
+#pragma unroll
+    for (int j = 0; j < TPL; j++) q4_load_act(act[j], xq, xd, xs, (sub + LPR * j) >> 2, q);
+
+    uint4 hdr[U][TPL], q0[U][TPL], q1[U][TPL];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        int row = base + u * R + rr;
+        row = row < F ? row : F - 1;
+#pragma unroll
+        for (int j = 0; j < TPL; j++) {
+            const uint8_t *blk = mat + (size_t)row * RB + (size_t)((sub + LPR * j) >> 2) * Q4K_BYTES;
+            hdr[u][j] = ld16(blk);
+            q0[u][j] = ld16(blk + 16 + 32 * q);
+            q1[u][j] = ld16(blk + 32 + 32 * q);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < TPL; j++) v += q4_task(hdr[u][j], q0[u][j], q1[u][j], act[j], q);
+        v = group_sum<LPR>(v);
+        // swap(A=v, B=v) exchanges A's upper half with B's lower half, so
+        // the new B holds the upper-half (up-row) values in lanes < 32
+        auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        const float other = __uint_as_float(p[1]);
+        const int row = base + u * R + rr;
+        if (half == 0 && sub == 0 && row < F) {
+            const float g = v, up = other;
+            h[(size_t)slot * F + row] = (g / (1.0f + expf(-g))) * up;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ down --
+template <int WT>
+struct DownTask;
+
+template <>
+struct DownTask<QMAG_TYPE_Q4_K> {
+    static constexpr int BLOCK = Q4K_BYTES;
+    __device__ static float dot(const uint8_t *blk, const int8_t *hq, const float *hd,
+                                const int16_t *hs, int ib, int q)
+    {
+        Q4Act a;
+        q4_load_act(a, hq, hd, hs, ib, q);
+        const uint4 hdr = ld16(blk), q0 = ld16(blk + 16 + 32 * q), q1 = ld16(blk + 32 + 32 * q);
+        return q4_task(hdr, q0, q1, a, q);
+    }
+};
+
+template <>
+struct DownTask<QMAG_TYPE_Q6_K> {
+    static constexpr int BLOCK = Q6K_BYTES;
+    __device__ static float dot(const uint8_t *blk, const int8_t *hq, const float *hd,
+                                const int16_t *, int ib, int q)
+    {
+        Q6Act a;
+        q6_load_act(a, hq, ib, q >> 1, q & 1);
+        Q6Raw r;
+        q6_load_raw(r, blk, q >> 1, q & 1);
+        const int isum = group_sum_i<4>(q6_int_dot(r, a, q & 1));
+        return q == 0 ? h2f(r.d) * hd[ib] * (float)isum : 0.0f;
+    }
+};
+
+template <int NBF, int TD, int TDS>
+__global__ __launch_bounds__(256) void down_kernel(const uint8_t *__restrict__ down_exps,
+                                                   const uint8_t *__restrict__ down_sh,
+                                                   const int *__restrict__ sel,
+                                                   const float *__restrict__ w,
+                                                   const float *__restrict__ gs, int K, int N,
+                                                   const int8_t *__restrict__ hq,
+                                                   const float *__restrict__ hd,
+                                                   const int16_t *__restrict__ hs,
+                                                   const float *resid, float *out)
+{
+    constexpr int TPR = 4 * NBF;             // tasks per (row, slot) dot
+    constexpr int LPR = TPR;                 // NBF in {1, 2, 4}
+    constexpr int RPW = 64 / LPR;
+    constexpr int F = NBF * QK_K;
+    const int lane = lane_id();
+    const int sub = lane % LPR, rw = lane / LPR, q = sub & 3, ib = sub >> 2;
+    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int row = wave * RPW + rw;
+    if (wave * RPW >= N) return;               // wave-uniform
+    const int rowc = row < N ? row : N - 1;
+
+    float acc = 0.0f;
+    for (int k = 0; k < K; k++) {
+        const size_t slab = (size_t)N * NBF * DownTask<TD>::BLOCK;
+        const uint8_t *blk = down_exps + (size_t)sel[k] * slab +
+                             ((size_t)rowc * NBF + ib) * DownTask<TD>::BLOCK;
+        const float d = group_sum<LPR>(DownTask<TD>::dot(blk, hq + (size_t)k * F, hd + (size_t)k * NBF,
+                                                         hs + (size_t)k * (F / 16), ib, q));
+        acc = __fadd_rn(acc, __fmul_rn(w[k], d));
+    }
+    {
+        const uint8_t *blk = down_sh + ((size_t)rowc * NBF + ib) * DownTask<TDS>::BLOCK;
+        const float d = group_sum<LPR>(DownTask<TDS>::dot(blk, hq + (size_t)K * F, hd + (size_t)K * NBF,
+                                                          hs + (size_t)K * (F / 16), ib, q));
+        acc = __fadd_rn(acc, __fmul_rn(gs[0], d));
+    }
+    if (sub == 0 && row < N) out[row] = resid ? __fadd_rn(acc, resid[row]) : acc;
+}
+
+// ------------------------------------------------------------------ host --
+static bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
+
+int moe_check_layer(const qmag_moe_layer *L)
+{
+    if (!L) return fail(QMAG_ERR_ARG, "moe: null layer");
+    if (L->n_embd % QK_K || !pow2_in(L->n_embd / QK_K, 1, 16))
+        return fail(QMAG_ERR_ARG, "moe: n_embd=%d unsupported (256..4096, power of two)", L->n_embd);
+    if (L->n_ff % QK_K || !pow2_in(L->n_ff / QK_K, 1, 4))
+        return fail(QMAG_ERR_ARG, "moe: n_ff=%d unsupported (256, 512, 1024)", L->n_ff);
+    if (L->n_expert < 1 || L->n_expert > 256) return fail(QMAG_ERR_ARG, "moe: n_expert=%d", L->n_expert);
+    if (L->n_used < 1 || L->n_used > 8 || L->n_used > L->n_expert)
+        return fail(QMAG_ERR_ARG, "moe: n_used=%d", L->n_used);
+    for (int t : {L->t_down_exps, L->t_down_shexp})
+        if (t != QMAG_TYPE_Q4_K && t != QMAG_TYPE_Q6_K) return fail(QMAG_ERR_ARG, "moe: down type %d", t);
+    if (!L->gate_inp || !L->gate_exps || !L->up_exps || !L->down_exps || !L->gate_inp_shexp ||
+        !L->gate_shexp || !L->up_shexp || !L->down_shexp)
+        return fail(QMAG_ERR_ARG, "moe: null tensor pointer");
+    return QMAG_OK;
+}
+
+struct MoeWs {
+    float *logits, *w, *gs, *h, *hd;
+    int *sel;
+    int8_t *xq, *hq;
+    float *xd;
+    int16_t *xs, *hs;
+};
+
+static int moe_ws(const qmag_moe_layer *L, int T, MoeWs &ws)
+{
+    const int N = L->n_embd, F = L->n_ff, E = L->n_expert, K = L->n_used, S = K + 1;
+    int st;
+#define WS(field, type, slot, count)                                              \
+    ws.field = (type *)workspace(slot, sizeof(type) * (size_t)(count), &st);      \
+    if (st) return st;
+    WS(logits, float, WS_LOGITS, (size_t)T * E);
+    WS(sel, int, WS_SEL, (size_t)T * K);
+    WS(w, float, WS_W, (size_t)T * K);
+    WS(gs, float, WS_GS, T);
+    WS(xq, int8_t, WS_XQ, (size_t)T * N);
+    WS(xd, float, WS_XD, (size_t)T * (N / QK_K));
+    WS(xs, int16_t, WS_XS, (size_t)T * (N / 16));
+    WS(h, float, WS_H, (size_t)T * S * F);
+    WS(hq, int8_t, WS_HQ, (size_t)T * S * F);
+    WS(hd, float, WS_HD, (size_t)T * S * (F / QK_K));
+    WS(hs, int16_t, WS_HS, (size_t)T * S * (F / 16));
+#undef WS
+    return QMAG_OK;
+}
+
+static MoeWs g_last;
+static int g_last_K = 0;
+
+template <int NBE>
+static void launch_gateup(const qmag_moe_layer *L, const MoeWs &ws, int t, hipStream_t s)
+{
+    constexpr int TPR = 4 * NBE;
+    constexpr int LPR = TPR < 32 ? TPR : 32;
+    constexpr int R = 32 / LPR;
+    const int N = L->n_embd, F = L->n_ff, K = L->n_used, S = K + 1;
+    const int steps = (F + R * 2 - 1) / (R * 2);
+    const int waves = steps * S;
+    hipLaunchKernelGGL(gateup_kernel<NBE>, dim3((waves + 3) / 4), dim3(256), 0, s,
+                       (const uint8_t *)L->gate_exps, (const uint8_t *)L->up_exps,
+                       (const uint8_t *)L->gate_shexp, (const uint8_t *)L->up_shexp,
+                       ws.sel + (size_t)t * K, K, F, ws.xq + (size_t)t * N, ws.xd + (size_t)t * (N / QK_K),
+                       ws.xs + (size_t)t * (N / 16), ws.h + (size_t)t * S * F);
+}
+
+template <int NBF, int TD, int TDS>
+static void launch_down3(const qmag_moe_layer *L, const MoeWs &ws, int t, const float *resid,
+                         float *out, hipStream_t s)
+{
+    const int N = L->n_embd, F = L->n_ff, K = L->n_used, S = K + 1;
+    constexpr int RPW = 64 / (4 * NBF);
+    const int waves = (N + RPW - 1) / RPW;
+    // one wave per workgroup: the grid is only N/RPW waves, spread it over CUs
+    hipLaunchKernelGGL((down_kernel<NBF, TD, TDS>), dim3(waves), dim3(64), 0, s,
+                       (const uint8_t *)L->down_exps, (const uint8_t *)L->down_shexp,
+                       ws.sel + (size_t)t * K, ws.w + (size_t)t * K, ws.gs + t, K, N,
+                       ws.hq + (size_t)t * S * F, ws.hd + (size_t)t * S * (F / QK_K),
+                       ws.hs + (size_t)t * S * (F / 16), resid ? resid + (size_t)t * N : nullptr,
+                       out + (size_t)t * N);
+}
+
+template <int NBF>
+static void launch_down2(const qmag_moe_layer *L, const MoeWs &ws, int t, const float *resid,
+                         float *out, hipStream_t s)
+{
+    const bool r6 = L->t_down_exps == QMAG_TYPE_Q6_K, s6 = L->t_down_shexp == QMAG_TYPE_Q6_K;
+    if (r6 && s6) launch_down3<NBF, QMAG_TYPE_Q6_K, QMAG_TYPE_Q6_K>(L, ws, t, resid, out, s);
+    else if (r6) launch_down3<NBF, QMAG_TYPE_Q6_K, QMAG_TYPE_Q4_K>(L, ws, t, resid, out, s);
+    else if (s6) launch_down3<NBF, QMAG_TYPE_Q4_K, QMAG_TYPE_Q6_K>(L, ws, t, resid, out, s);
+    else launch_down3<NBF, QMAG_TYPE_Q4_K, QMAG_TYPE_Q4_K>(L, ws, t, resid, out, s);
+}
+
+int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const float *resid,
+            hipStream_t s)
+{
+    int st = moe_check_layer(L);
+    if (st) return st;
+    if (T <= 0 || !x || !out) return fail(QMAG_ERR_ARG, "moe: T=%d x=%p out=%p", T, x, out);
+    MoeWs ws;
+    st = moe_ws(L, T, ws);
+    if (st) return st;
+    const int N = L->n_embd, F = L->n_ff, E = L->n_expert, K = L->n_used, S = K + 1;
+
+    prof_begin(PROF_ROUTER, s);
+    hipLaunchKernelGGL(router_kernel, dim3((E * T + 3) / 4), dim3(256), 0, s, L->gate_inp,
+                       L->router_bias, x, N, E, T, ws.logits);
+    prof_end(PROF_ROUTER, s);
+    prof_begin(PROF_TOPK, s);
+    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(256), 0, s, ws.logits, x, L->gate_inp_shexp, N,
+                       E, K, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs);
+    prof_end(PROF_TOPK, s);
+    for (int t = 0; t < T; t++) {
+        prof_begin(PROF_GATEUP, s);
+        switch (N / QK_K) {
+        case 1: launch_gateup<1>(L, ws, t, s); break;
+        case 2: launch_gateup<2>(L, ws, t, s); break;
+        case 4: launch_gateup<4>(L, ws, t, s); break;
+        case 8: launch_gateup<8>(L, ws, t, s); break;
+        default: launch_gateup<16>(L, ws, t, s); break;
+        }
+        prof_end(PROF_GATEUP, s);
+        prof_begin(PROF_HQUANT, s);
+        st = launch_q8k_quant(ws.h + (size_t)t * S * F, S * (F / QK_K), ws.hq + (size_t)t * S * F,
+                              ws.hd + (size_t)t * S * (F / QK_K), ws.hs + (size_t)t * S * (F / 16), s);
+        prof_end(PROF_HQUANT, s);
+        if (st) return st;
+        prof_begin(PROF_DOWN, s);
+        switch (F / QK_K) {
+        case 1: launch_down2<1>(L, ws, t, resid, out, s); break;
+        case 2: launch_down2<2>(L, ws, t, resid, out, s); break;
+        default: launch_down2<4>(L, ws, t, resid, out, s); break;
+        }
+        prof_end(PROF_DOWN, s);
+    }
+    QMAG_HIP(hipGetLastError());
+    g_last = ws;
+    g_last_K = K;
+    return QMAG_OK;
+}
+
+}  // namespace qmag
+
+using namespace qmag;
+
+extern "C" int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *out, int T)
+{
+    int st = require_ready();
+    if (st) return st;
+    return moe_ffn(L, x, out, T, nullptr, ctx().stream);
+}
+
+extern "C" int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, float *x, int n_tok)
+{
+    int st = require_ready();
+    if (st) return st;
+    if (!layers || n_layer <= 0 || n_tok <= 0 || !x) return fail(QMAG_ERR_ARG, "moe_stack: bad args");
+    for (int l = 0; l < n_layer; l++) {
+        st = moe_check_layer(&layers[l]);
+        if (st) return st;
+    }
+    const int N = layers[0].n_embd;
+    for (int t = 0; t < n_tok; t++) {
+        float *xt = x + (size_t)t * N;
+        for (int l = 0; l < n_layer; l++) {
+            st = moe_ffn(&layers[l], xt, xt, 1, xt, ctx().stream);
+            if (st) return st;
+        }
+    }
+    return QMAG_OK;
+}
+
+extern "C" int qmag_moe_last_stage(const float **logits, const int **sel, const float **w,
+                                   const float **gs, const float **h)
+{
+    if (!g_last.logits) return fail(QMAG_ERR_ARG, "no MoE call yet");
+    if (logits) *logits = g_last.logits;
+    if (sel) *sel = g_last.sel;
+    if (w) *w = g_last.w;
+    if (gs) *gs = g_last.gs;
+    if (h) *h = g_last.h;
+    return QMAG_OK;
+}

@@ -1,0 +1,435 @@
+// qmag_runtime.hip -- device selection, errors, memory, events, and the
+// reference-compatible qma_q8k_* entries (src/q8k.c:271-316).
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "qmag_internal.h"
+
+namespace qmag {
+
+static Ctx g_ctx;
+static std::mutex g_mu;
+static thread_local char t_err[512] = "no error";
+static void *g_ws[WS_COUNT] = {};
+static size_t g_ws_cap[WS_COUNT] = {};
+
+Ctx &ctx() { return g_ctx; }
+
+int fail(int code, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof(t_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what, const char *file, int line)
+{
+    return fail(QMAG_ERR_HIP, "%s failed: %s (%s:%d)", what, hipGetErrorString(e), file, line);
+}
+
+int require_ready()
+{
+    if (!g_ctx.ready) return fail(QMAG_ERR_NODEV, "qmag_init() has not succeeded");
+    return QMAG_OK;
+}
+
+void *workspace(int slot, size_t bytes, int *status)
+{
+    *status = QMAG_OK;
+    if (bytes <= g_ws_cap[slot]) return g_ws[slot];
+    size_t cap = bytes < 4096 ? 4096 : bytes;
+    cap = (cap + 4095) & ~(size_t)4095;
+    if (g_ws[slot]) {
+        hipError_t e = hipStreamSynchronize(g_ctx.stream);
+        if (e == hipSuccess) e = hipFree(g_ws[slot]);
+        if (e != hipSuccess) {
+            *status = hip_fail(e, "workspace free", __FILE__, __LINE__);
+            return nullptr;
+        }
+        g_ws[slot] = nullptr;
+        g_ws_cap[slot] = 0;
+    }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, cap);
+    if (e != hipSuccess) {
+        *status = hip_fail(e, "workspace hipMalloc", __FILE__, __LINE__);
+        return nullptr;
+    }
+    g_ws[slot] = p;
+    g_ws_cap[slot] = cap;
+    return p;
+}
+
+// Event pairs recorded around kernels while profiling; reduced on read.
+struct ProfRec {
+    int id;
+    hipEvent_t a, b;
+};
+static bool g_prof = false;
+static std::vector<ProfRec> g_prof_recs;
+static std::vector<hipEvent_t> g_prof_free;
+static long g_prof_count[PROF_COUNT];
+static double g_prof_ms[PROF_COUNT];
+static hipEvent_t g_prof_open[PROF_COUNT];
+
+bool prof_on() { return g_prof; }
+
+static hipEvent_t prof_event()
+{
+    hipEvent_t e = nullptr;
+    if (!g_prof_free.empty()) {
+        e = g_prof_free.back();
+        g_prof_free.pop_back();
+    } else if (hipEventCreate(&e) != hipSuccess) {
+        e = nullptr;
+    }
+    return e;
+}
+
+void prof_begin(int id, hipStream_t s)
+{
+    if (!g_prof) return;
+    hipEvent_t e = prof_event();
+    if (e && hipEventRecord(e, s) == hipSuccess) g_prof_open[id] = e;
+}
+
+void prof_end(int id, hipStream_t s)
+{
+    if (!g_prof || !g_prof_open[id]) return;
+    hipEvent_t e = prof_event();
+    if (e && hipEventRecord(e, s) == hipSuccess) g_prof_recs.push_back({id, g_prof_open[id], e});
+    g_prof_open[id] = nullptr;
+}
+
+static int prof_reduce()
+{
+    for (auto &r : g_prof_recs) {
+        QMAG_HIP(hipEventSynchronize(r.b));
+        float ms = 0.0f;
+        QMAG_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+        g_prof_count[r.id]++;
+        g_prof_ms[r.id] += ms;
+        g_prof_free.push_back(r.a);
+        g_prof_free.push_back(r.b);
+    }
+    g_prof_recs.clear();
+    return QMAG_OK;
+}
+
+}  // namespace qmag
+
+using namespace qmag;
+
+int qmag_prof_enable(int on)
+{
+    int st = require_ready();
+    if (st) return st;
+    st = prof_reduce();
+    if (st) return st;
+    if (on) {
+        for (int i = 0; i < PROF_COUNT; i++) {
+            g_prof_count[i] = 0;
+            g_prof_ms[i] = 0.0;
+        }
+    }
+    g_prof = on != 0;
+    return QMAG_OK;
+}
+
+int qmag_prof_read(int id, long *count, double *total_ms)
+{
+    int st = require_ready();
+    if (st) return st;
+    if (id < 0 || id >= PROF_COUNT) return fail(QMAG_ERR_ARG, "prof id %d", id);
+    st = prof_reduce();
+    if (st) return st;
+    if (count) *count = g_prof_count[id];
+    if (total_ms) *total_ms = g_prof_ms[id];
+    return QMAG_OK;
+}
+
+extern "C" {
+
+const char *qmag_last_error(void) { return t_err; }
+
+int qmag_init(int device)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_ctx.ready) return g_ctx.dev == device ? QMAG_OK : fail(QMAG_ERR_ARG, "already initialised on device %d", g_ctx.dev);
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= device || device < 0)
+        return fail(QMAG_ERR_NODEV, "no HIP device %d (count %d, %s)", device, n,
+                    e == hipSuccess ? "ok" : hipGetErrorString(e));
+    hipDeviceProp_t prop;
+    QMAG_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(QMAG_ERR_NODEV, "device %d is %s; this library is built for gfx950", device,
+                    prop.gcnArchName);
+    QMAG_HIP(hipSetDevice(device));
+    QMAG_HIP(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
+    for (int i = 0; i < 64; i++) QMAG_HIP(hipEventCreate(&g_ctx.ev[i]));
+    g_ctx.dev = device;
+    g_ctx.n_cu = prop.multiProcessorCount;
+    g_ctx.clock_khz = prop.clockRate;
+    g_ctx.hbm = prop.totalGlobalMem;
+    snprintf(g_ctx.arch, sizeof(g_ctx.arch), "%s", prop.gcnArchName);
+    g_ctx.ready = true;
+    return QMAG_OK;
+}
+
+int qmag_device_info(int *n_cu, int *clock_khz, size_t *hbm_bytes, char *arch, int arch_len)
+{
+    int st = require_ready();
+    if (st) return st;
+    if (n_cu) *n_cu = g_ctx.n_cu;
+    if (clock_khz) *clock_khz = g_ctx.clock_khz;
+    if (hbm_bytes) *hbm_bytes = g_ctx.hbm;
+    if (arch && arch_len > 0) snprintf(arch, (size_t)arch_len, "%s", g_ctx.arch);
+    return QMAG_OK;
+}
+
+int qmag_malloc(void **dptr, size_t bytes)
+{
+    int st = require_ready();
+    if (st) return st;
+    QMAG_HIP(hipMalloc(dptr, bytes));
+    return QMAG_OK;
+}
+
+int qmag_free(void *dptr)
+{
+    int st = require_ready();
+    if (st) return st;
+    QMAG_HIP(hipStreamSynchronize(g_ctx.stream));
+    QMAG_HIP(hipFree(dptr));
+    return QMAG_OK;
+}
+
+int qmag_h2d(void *dst, const void *src, size_t bytes)
+{
+    int st = require_ready();
+    if (st) return st;
+    QMAG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx.stream));
+    QMAG_HIP(hipStreamSynchronize(g_ctx.stream));
+    return QMAG_OK;
+}
+
+int qmag_d2h(void *dst, const void *src, size_t bytes)
+{
+    int st = require_ready();
+    if (st) return st;
+    QMAG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.stream));
+    QMAG_HIP(hipStreamSynchronize(g_ctx.stream));
+    return QMAG_OK;
+}
+
+int qmag_d2d(void *dst, const void *src, size_t bytes)
+{
+    int st = require_ready();
+    if (st) return st;
+    QMAG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_ctx.stream));
+    return QMAG_OK;
+}
+
+int qmag_memset(void *dst, int value, size_t bytes)
+{
+    int st = require_ready();
+    if (st) return st;
+    QMAG_HIP(hipMemsetAsync(dst, value, bytes, g_ctx.stream));
+    return QMAG_OK;
+}
+
+int qmag_sync(void)
+{
+    int st = require_ready();
+    if (st) return st;
+    QMAG_HIP(hipStreamSynchronize(g_ctx.stream));
+    return QMAG_OK;
+}
+
+int qmag_event_record(int slot)
+{
+    int st = require_ready();
+    if (st) return st;
+    if (slot < 0 || slot >= 64) return fail(QMAG_ERR_ARG, "event slot %d out of range", slot);
+    QMAG_HIP(hipEventRecord(g_ctx.ev[slot], g_ctx.stream));
+    return QMAG_OK;
+}
+
+int qmag_event_elapsed(int a, int b, float *ms)
+{
+    int st = require_ready();
+    if (st) return st;
+    if (a < 0 || a >= 64 || b < 0 || b >= 64) return fail(QMAG_ERR_ARG, "event slot out of range");
+    QMAG_HIP(hipEventSynchronize(g_ctx.ev[b]));
+    QMAG_HIP(hipEventElapsedTime(ms, g_ctx.ev[a], g_ctx.ev[b]));
+    return QMAG_OK;
+}
+
+int qmag_q8k_quant_dev(const float *x, int n, int T, int8_t *xq, float *xd, int16_t *xsum)
+{
+    int st = require_ready();
+    if (st) return st;
+    if (n <= 0 || n % QK_K || T <= 0) return fail(QMAG_ERR_ARG, "q8k_quant: n=%d T=%d", n, T);
+    return launch_q8k_quant(x, (n / QK_K) * T, xq, xd, xsum, g_ctx.stream);
+}
+
+int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
+                        int n_in, int n_out, int T, int wtype, float *out)
+{
+    int st = require_ready();
+    if (st) return st;
+    return launch_matvec(xq, xd, xsum, W, n_in, n_out, T, wtype, out, g_ctx.stream);
+}
+
+int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype, float *out)
+{
+    int st = require_ready();
+    if (st) return st;
+    if (n_in <= 0 || n_in % QK_K || T <= 0) return fail(QMAG_ERR_ARG, "matmul: n_in=%d T=%d", n_in, T);
+    int8_t *xq = (int8_t *)workspace(WS_XQ, (size_t)T * n_in, &st);
+    if (st) return st;
+    float *xd = (float *)workspace(WS_XD, sizeof(float) * (size_t)T * (n_in / QK_K), &st);
+    if (st) return st;
+    int16_t *xs = (int16_t *)workspace(WS_XS, sizeof(int16_t) * (size_t)T * (n_in / 16), &st);
+    if (st) return st;
+    st = launch_q8k_quant(x, (n_in / QK_K) * T, xq, xd, xs, g_ctx.stream);
+    if (st) return st;
+    return launch_matvec(xq, xd, xs, W, n_in, n_out, T, wtype, out, g_ctx.stream);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Reference-compatible per-row entries.  Each calling thread gets its own  */
+/* stream and staging buffer, so concurrent calls from a CPU pool (as      */
+/* nn.c:276-289 and nn.c:652-706 make them) do not share state.            */
+/* ---------------------------------------------------------------------- */
+
+struct Staging {
+    hipStream_t s = nullptr;
+    uint8_t *dev = nullptr;
+    size_t cap = 0;
+    ~Staging()
+    {
+        if (dev) (void)hipFree(dev);
+        if (s) (void)hipStreamDestroy(s);
+    }
+};
+static thread_local Staging t_stage;
+
+static uint8_t *stage(size_t bytes)
+{
+    if (!t_stage.s && hipStreamCreateWithFlags(&t_stage.s, hipStreamNonBlocking) != hipSuccess)
+        return nullptr;
+    if (bytes > t_stage.cap) {
+        if (t_stage.dev) (void)hipFree(t_stage.dev);
+        t_stage.dev = nullptr;
+        t_stage.cap = 0;
+        size_t cap = (bytes + 65535) & ~(size_t)65535;
+        if (hipMalloc(&t_stage.dev, cap) != hipSuccess) return nullptr;
+        t_stage.cap = cap;
+    }
+    return t_stage.dev;
+}
+
+[[noreturn]] static void compat_abort(const char *fn)
+{
+    fprintf(stderr, "libqmagpu: %s called without a usable gfx950 device (%s); "
+                    "callers must check qma_q8k_available() first\n", fn, t_err);
+    abort();
+}
+
+static void ensure_ready_or_abort(const char *fn)
+{
+    if (!g_ctx.ready && qmag_init(0) != QMAG_OK) compat_abort(fn);
+}
+
+static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int qma_q8k_available(void)
+{
+    if (g_ctx.ready) return 1;
+    return qmag_init(0) == QMAG_OK ? 1 : 0;
+}
+
+void qma_q8k_quant(const float *x, int n, int8_t *xq, float *xd, int16_t *xsum)
+{
+    ensure_ready_or_abort("qma_q8k_quant");
+    if (n <= 0) return;
+    const int nb = n / QK_K;
+    const size_t ox = 0, oq = a256(sizeof(float) * (size_t)n), od = oq + a256((size_t)n),
+                 os = od + a256(sizeof(float) * (size_t)nb), tot = os + a256(sizeof(int16_t) * (size_t)(n / 16));
+    uint8_t *b = stage(tot);
+    if (!b) compat_abort("qma_q8k_quant");
+    hipStream_t s = t_stage.s;
+    bool ok = hipMemcpyAsync(b + ox, x, sizeof(float) * (size_t)n, hipMemcpyHostToDevice, s) == hipSuccess;
+    ok = ok && launch_q8k_quant((const float *)(b + ox), nb, (int8_t *)(b + oq), (float *)(b + od),
+                                (int16_t *)(b + os), s) == QMAG_OK;
+    ok = ok && hipMemcpyAsync(xq, b + oq, (size_t)nb * QK_K, hipMemcpyDeviceToHost, s) == hipSuccess;
+    ok = ok && hipMemcpyAsync(xd, b + od, sizeof(float) * (size_t)nb, hipMemcpyDeviceToHost, s) == hipSuccess;
+    ok = ok && hipMemcpyAsync(xsum, b + os, sizeof(int16_t) * (size_t)nb * 16, hipMemcpyDeviceToHost, s) == hipSuccess;
+    ok = ok && hipStreamSynchronize(s) == hipSuccess;
+    if (!ok) compat_abort("qma_q8k_quant");
+}
+
+// stage rows + activation, run the matvec kernel over n_rows rows, copy back
+static void compat_dot(const void *const *rows, int n_rows, int wtype, const int8_t *xq,
+                       const float *xd, const int16_t *xsum, int n, float *out, const char *fn)
+{
+    ensure_ready_or_abort(fn);
+    const int nb = n / QK_K;
+    const size_t rb = (size_t)nb * (wtype == QMAG_TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES);
+    const size_t ow = 0, oq = a256(rb * (size_t)n_rows), od = oq + a256((size_t)n),
+                 os = od + a256(sizeof(float) * (size_t)nb), oo = os + a256(sizeof(int16_t) * (size_t)(n / 16)),
+                 tot = oo + a256(sizeof(float) * (size_t)n_rows);
+    uint8_t *b = stage(tot);
+    if (!b) compat_abort(fn);
+    hipStream_t s = t_stage.s;
+    bool ok = true;
+    for (int r = 0; r < n_rows && ok; r++)
+        ok = hipMemcpyAsync(b + ow + rb * (size_t)r, rows[r], rb, hipMemcpyHostToDevice, s) == hipSuccess;
+    ok = ok && hipMemcpyAsync(b + oq, xq, (size_t)n, hipMemcpyHostToDevice, s) == hipSuccess;
+    ok = ok && hipMemcpyAsync(b + od, xd, sizeof(float) * (size_t)nb, hipMemcpyHostToDevice, s) == hipSuccess;
+    if (xsum)
+        ok = ok && hipMemcpyAsync(b + os, xsum, sizeof(int16_t) * (size_t)(n / 16), hipMemcpyHostToDevice, s) == hipSuccess;
+    else
+        ok = ok && hipMemsetAsync(b + os, 0, sizeof(int16_t) * (size_t)(n / 16), s) == hipSuccess;
+    ok = ok && launch_matvec((const int8_t *)(b + oq), (const float *)(b + od), (const int16_t *)(b + os),
+                             b + ow, n, n_rows, 1, wtype, (float *)(b + oo), s) == QMAG_OK;
+    ok = ok && hipMemcpyAsync(out, b + oo, sizeof(float) * (size_t)n_rows, hipMemcpyDeviceToHost, s) == hipSuccess;
+    ok = ok && hipStreamSynchronize(s) == hipSuccess;
+    if (!ok) compat_abort(fn);
+}
+
+float qma_q8k_dot(const void *row, int wtype, const int8_t *xq, const float *xd,
+                  const int16_t *xsum, int n)
+{
+    if (wtype != QMAG_TYPE_Q4_K && wtype != QMAG_TYPE_Q6_K) return 0.0f;   // q8k.c:314-315
+    if (n <= 0) return 0.0f;
+    float out = 0.0f;
+    compat_dot(&row, 1, wtype, xq, xd, xsum, n, &out, "qma_q8k_dot");
+    return out;
+}
+
+void qma_q8k_gateup(const void *g, const void *u, const int8_t *xq, const float *xd,
+                    const int16_t *xsum, int n, float *gate, float *up)
+{
+    if (n <= 0) {
+        *gate = *up = 0.0f;
+        return;
+    }
+    const void *rows[2] = {g, u};
+    float out[2];
+    compat_dot(rows, 2, QMAG_TYPE_Q4_K, xq, xd, xsum, n, out, "qma_q8k_gateup");
+    *gate = out[0];
+    *up = out[1];
+}
+
+}  // extern "C"

@@ -1,0 +1,320 @@
+"""Python host-side binding of libqmagpu.so (ctypes), mirroring the C-ABI in
+include/qma_gpu.h: the reference-compatible qma_q8k_* entries (src/q8k.c)
+and the device entries for the matmul / moe_ffn seams of src/nn.c.
+
+There is no fallback: if libqmagpu.so is missing or no gfx950 device is
+present, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqmagpu.so")
+
+QK_K = 256
+TYPE_Q4_K = 12
+TYPE_Q6_K = 14
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
+
+P = C.c_void_p
+
+# name -> (restype, argtypes); every symbol the header declares
+SIGNATURES = {
+    "qma_q8k_available": (C.c_int, []),
+    "qma_q8k_quant": (None, [P, C.c_int, P, P, P]),
+    "qma_q8k_dot": (C.c_float, [P, C.c_int, P, P, P, C.c_int]),
+    "qma_q8k_gateup": (None, [P, P, P, P, P, C.c_int, P, P]),
+    "qmag_init": (C.c_int, [C.c_int]),
+    "qmag_last_error": (C.c_char_p, []),
+    "qmag_device_info": (C.c_int, [P, P, P, C.c_char_p, C.c_int]),
+    "qmag_malloc": (C.c_int, [C.POINTER(P), C.c_size_t]),
+    "qmag_free": (C.c_int, [P]),
+    "qmag_h2d": (C.c_int, [P, P, C.c_size_t]),
+    "qmag_d2h": (C.c_int, [P, P, C.c_size_t]),
+    "qmag_d2d": (C.c_int, [P, P, C.c_size_t]),
+    "qmag_memset": (C.c_int, [P, C.c_int, C.c_size_t]),
+    "qmag_sync": (C.c_int, []),
+    "qmag_event_record": (C.c_int, [C.c_int]),
+    "qmag_event_elapsed": (C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_float)]),
+    "qmag_prof_enable": (C.c_int, [C.c_int]),
+    "qmag_prof_read": (C.c_int, [C.c_int, C.POINTER(C.c_long), C.POINTER(C.c_double)]),
+    "qmag_q8k_quant_dev": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
+    "qmag_matmul_q8k_dev": (C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+    "qmag_matmul_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+    "qmag_moe_ffn_dev": (C.c_int, [P, P, P, C.c_int]),
+    "qmag_moe_stack_dev": (C.c_int, [P, C.c_int, P, C.c_int]),
+    "qmag_moe_last_stage": (C.c_int, [C.POINTER(P)] * 5),
+    "qmag_synth_normal": (C.c_int, [C.c_uint64, C.c_size_t, C.c_float, C.c_float, P]),
+    "qmag_synth_weights": (C.c_int, [C.c_uint64, C.c_size_t, C.c_float, C.c_int, P]),
+    "qmag_quantize_dev": (C.c_int, [P, C.c_size_t, C.c_int, P]),
+}
+
+
+class QmagError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise QmagError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != 0:
+        raise QmagError(f"qmag status {status}: {lib().qmag_last_error().decode()}")
+
+
+def init(device: int = 0) -> None:
+    check(lib().qmag_init(device))
+
+
+def device_info():
+    n_cu, clk, hbm = C.c_int(), C.c_int(), C.c_size_t()
+    arch = C.create_string_buffer(64)
+    check(lib().qmag_device_info(C.byref(n_cu), C.byref(clk), C.byref(hbm), arch, 64))
+    return dict(n_cu=n_cu.value, clock_khz=clk.value, hbm_bytes=hbm.value, arch=arch.value.decode())
+
+
+def sync() -> None:
+    check(lib().qmag_sync())
+
+
+class DBuf:
+    """A device allocation owned by Python (freed on close / GC)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = P()
+        check(lib().qmag_malloc(C.byref(p), max(self.nbytes, 1)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DBuf":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        check(lib().qmag_h2d(self.ptr + offset, a.ctypes.data_as(P), a.nbytes))
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        check(lib().qmag_d2h(out.ctypes.data_as(P), self.ptr + offset, out.nbytes))
+        return out
+
+    def at(self, offset: int) -> int:
+        return self.ptr + offset
+
+    def close(self) -> None:
+        if getattr(self, "ptr", None):
+            try:
+                lib().qmag_free(self.ptr)
+            finally:
+                self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def d2h_ptr(ptr: int, dtype, count: int) -> np.ndarray:
+    out = np.empty(count, dtype=np.dtype(dtype))
+    check(lib().qmag_d2h(out.ctypes.data_as(P), ptr, out.nbytes))
+    return out
+
+
+class MoeLayer(C.Structure):
+    """struct qmag_moe_layer (include/qma_gpu.h)."""
+    _fields_ = [
+        ("n_embd", C.c_int), ("n_ff", C.c_int), ("n_expert", C.c_int), ("n_used", C.c_int),
+        ("gate_inp", P), ("router_bias", P),
+        ("gate_exps", P), ("up_exps", P), ("down_exps", P), ("t_down_exps", C.c_int),
+        ("gate_inp_shexp", P), ("gate_shexp", P), ("up_shexp", P), ("down_shexp", P),
+        ("t_down_shexp", C.c_int),
+    ]
+
+
+# --------------------------------------------------------------- entries --
+
+def q8k_quant_dev(x: DBuf, n: int, T: int, xq: DBuf, xd: DBuf, xs: DBuf) -> None:
+    check(lib().qmag_q8k_quant_dev(x.ptr, n, T, xq.ptr, xd.ptr, xs.ptr))
+
+
+def matmul_q8k_dev(xq, xd, xs, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> None:
+    check(lib().qmag_matmul_q8k_dev(xq.ptr, xd.ptr, xs.ptr if xs is not None else None, W.ptr,
+                                    n_in, n_out, T, wtype, out.ptr))
+
+
+def matmul_dev(x: DBuf, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> None:
+    check(lib().qmag_matmul_dev(x.ptr, W.ptr, n_in, n_out, T, wtype, out.ptr))
+
+
+def moe_ffn_dev(layer: MoeLayer, x_ptr: int, out_ptr: int, T: int) -> None:
+    check(lib().qmag_moe_ffn_dev(C.byref(layer), x_ptr, out_ptr, T))
+
+
+def moe_stack_dev(layers, x_ptr: int, n_tok: int) -> None:
+    arr = (MoeLayer * len(layers))(*layers)
+    check(lib().qmag_moe_stack_dev(arr, len(layers), x_ptr, n_tok))
+
+
+def moe_last_stage(n_expert: int, n_used: int, n_ff: int):
+    ptrs = [P() for _ in range(5)]
+    check(lib().qmag_moe_last_stage(*[C.byref(p) for p in ptrs]))
+    logits = d2h_ptr(ptrs[0].value, np.float32, n_expert)
+    sel = d2h_ptr(ptrs[1].value, np.int32, n_used)
+    w = d2h_ptr(ptrs[2].value, np.float32, n_used)
+    gs = d2h_ptr(ptrs[3].value, np.float32, 1)[0]
+    h = d2h_ptr(ptrs[4].value, np.float32, (n_used + 1) * n_ff).reshape(n_used + 1, n_ff)
+    return dict(logits=logits, sel=sel, w=w, gs=gs, h=h)
+
+
+def synth_normal(seed: int, n: int, mean: float, std: float, out_ptr: int) -> None:
+    check(lib().qmag_synth_normal(C.c_uint64(seed), n, mean, std, out_ptr))
+
+
+def synth_weights(seed: int, n: int, std: float, wtype: int, out_ptr: int) -> None:
+    check(lib().qmag_synth_weights(C.c_uint64(seed), n, std, wtype, out_ptr))
+
+
+def quantize_dev(x_ptr: int, n: int, wtype: int, out_ptr: int) -> None:
+    check(lib().qmag_quantize_dev(x_ptr, n, wtype, out_ptr))
+
+
+PROF_IDS = {"router": 0, "topk": 1, "gateup": 2, "hquant": 3, "down": 4, "fused": 5}
+
+
+def prof_enable(on: bool) -> None:
+    check(lib().qmag_prof_enable(1 if on else 0))
+
+
+def prof_read(name: str):
+    n, ms = C.c_long(), C.c_double()
+    check(lib().qmag_prof_read(PROF_IDS[name], C.byref(n), C.byref(ms)))
+    return n.value, ms.value
+
+
+class Timer:
+    """HIP events on the library stream (the stream every qmag_* kernel runs on)."""
+
+    def __init__(self, a: int = 0, b: int = 1):
+        self.a, self.b = a, b
+
+    def start(self) -> None:
+        check(lib().qmag_event_record(self.a))
+
+    def stop_ms(self) -> float:
+        check(lib().qmag_event_record(self.b))
+        ms = C.c_float()
+        check(lib().qmag_event_elapsed(self.a, self.b, C.byref(ms)))
+        return float(ms.value)
+
+
+# ------------------------------------------------------- resident layers --
+
+def tensor_seed(seed: int, layer: int, tag: int) -> int:
+    return (seed * 0x100000001B3 + layer * 1000003 + tag * 7919 + 1) & 0xFFFFFFFFFFFFFFFF
+
+
+class ResidentLayer:
+    """One MoE layer's tensors generated directly in HBM (GGUF layout):
+    router f32 ~N(0, .02), experts ~N(0, .02) quantised to Q4_K (gate/up)
+    and Q4_K/Q6_K (down), shared gate f32 ~N(0, .02)."""
+
+    def __init__(self, seed: int, layer: int = 0, n_embd=2048, n_ff=512, n_expert=256, n_used=8,
+                 t_down=TYPE_Q6_K, router_bias_std: float | None = None):
+        N, F, E = n_embd, n_ff, n_expert
+        self.n_embd, self.n_ff, self.n_expert, self.n_used, self.t_down = N, F, E, n_used, t_down
+        gu = N // QK_K * BLOCK_BYTES[TYPE_Q4_K] * F
+        dn = F // QK_K * BLOCK_BYTES[t_down] * N
+        self.bytes_gate_slab, self.bytes_down_slab = gu, dn
+        self.gate_inp = DBuf(4 * E * N)
+        self.gate_exps = DBuf(gu * E)
+        self.up_exps = DBuf(gu * E)
+        self.down_exps = DBuf(dn * E)
+        self.gate_inp_shexp = DBuf(4 * N)
+        self.gate_shexp = DBuf(gu)
+        self.up_shexp = DBuf(gu)
+        self.down_shexp = DBuf(dn)
+        self.router_bias = DBuf(4 * E) if router_bias_std is not None else None
+        ts = lambda tag: tensor_seed(seed, layer, tag)
+        synth_normal(ts(1), E * N, 0.0, 0.02, self.gate_inp.ptr)
+        synth_weights(ts(2), E * F * N, 0.02, TYPE_Q4_K, self.gate_exps.ptr)
+        synth_weights(ts(3), E * F * N, 0.02, TYPE_Q4_K, self.up_exps.ptr)
+        synth_weights(ts(4), E * N * F, 0.02, t_down, self.down_exps.ptr)
+        synth_normal(ts(5), N, 0.0, 0.02, self.gate_inp_shexp.ptr)
+        synth_weights(ts(6), F * N, 0.02, TYPE_Q4_K, self.gate_shexp.ptr)
+        synth_weights(ts(7), F * N, 0.02, TYPE_Q4_K, self.up_shexp.ptr)
+        synth_weights(ts(8), N * F, 0.02, t_down, self.down_shexp.ptr)
+        if self.router_bias is not None:
+            synth_normal(ts(9), E, 0.0, router_bias_std, self.router_bias.ptr)
+        self.c = MoeLayer(N, F, E, n_used, self.gate_inp.ptr,
+                          self.router_bias.ptr if self.router_bias else None,
+                          self.gate_exps.ptr, self.up_exps.ptr, self.down_exps.ptr, t_down,
+                          self.gate_inp_shexp.ptr, self.gate_shexp.ptr, self.up_shexp.ptr,
+                          self.down_shexp.ptr, t_down)
+
+    @classmethod
+    def from_host(cls, hl) -> "ResidentLayer":
+        """Upload an oracle HostLayer (tests)."""
+        self = cls.__new__(cls)
+        self.n_embd, self.n_ff, self.n_expert, self.n_used = hl.n_embd, hl.n_ff, hl.n_expert, hl.n_used
+        self.t_down = hl.t_down_exps
+        for k in ("gate_inp", "gate_exps", "up_exps", "down_exps", "gate_inp_shexp", "gate_shexp",
+                  "up_shexp", "down_shexp"):
+            setattr(self, k, DBuf.from_array(getattr(hl, k)))
+        self.router_bias = DBuf.from_array(hl.router_bias) if "router_bias" in hl.arrays else None
+        self.c = MoeLayer(hl.n_embd, hl.n_ff, hl.n_expert, hl.n_used, self.gate_inp.ptr,
+                          self.router_bias.ptr if self.router_bias else None,
+                          self.gate_exps.ptr, self.up_exps.ptr, self.down_exps.ptr, hl.t_down_exps,
+                          self.gate_inp_shexp.ptr, self.gate_shexp.ptr, self.up_shexp.ptr,
+                          self.down_shexp.ptr, hl.t_down_shexp)
+        return self
+
+    def host_arrays(self) -> dict:
+        """Download every tensor (for the CPU oracle)."""
+        N, F, E = self.n_embd, self.n_ff, self.n_expert
+        out = dict(
+            gate_inp=self.gate_inp.download(np.float32),
+            gate_exps=self.gate_exps.download(np.uint8),
+            up_exps=self.up_exps.download(np.uint8),
+            down_exps=self.down_exps.download(np.uint8),
+            gate_inp_shexp=self.gate_inp_shexp.download(np.float32),
+            gate_shexp=self.gate_shexp.download(np.uint8),
+            up_shexp=self.up_shexp.download(np.uint8),
+            down_shexp=self.down_shexp.download(np.uint8),
+        )
+        if self.router_bias is not None:
+            out["router_bias"] = self.router_bias.download(np.float32)
+        return out
+
+    def close(self) -> None:
+        for k in ("gate_inp", "gate_exps", "up_exps", "down_exps", "gate_inp_shexp", "gate_shexp",
+                  "up_shexp", "down_shexp", "router_bias"):
+            b = getattr(self, k, None)
+            if b is not None:
+                b.close()

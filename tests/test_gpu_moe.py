@@ -1,0 +1,136 @@
+"""GPU parity of the MoE FFN layer (nn.c:509-707) and the decode layer stack,
+through the C-ABI, against the CPU oracle on the same bytes.
+
+Stage-wise: router logits (fp32, 1e-4 of max|logit|), the top-n_used
+selection (exact, whenever the oracle's n_used-th / next probability gap is
+not a near-tie), renormalised weights, shared gate, h = silu(g)*u per slot,
+and the layer output (1e-4 of max|y|)."""
+import numpy as np
+import pytest
+
+from conftest import max_rel_err
+from moe_fixtures import make_host_layer
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+TIE = 1e-5        # relative probability gap below which a selection flip is a near-tie
+
+
+def route_margin(logits, n_used):
+    lg = logits.astype(np.float64)
+    p = np.exp(lg - lg.max())
+    p /= p.sum()
+    s = np.sort(p)[::-1]
+    return (s[n_used - 1] - s[n_used]) / s[n_used - 1]
+
+
+def host_of(orc, rl):
+    a = rl.host_arrays()
+    return orc.HostLayer(rl.n_embd, rl.n_ff, rl.n_expert, rl.n_used, a["gate_inp"], a["gate_exps"],
+                         a["up_exps"], a["down_exps"], rl.t_down, a["gate_inp_shexp"],
+                         a["gate_shexp"], a["up_shexp"], a["down_shexp"], rl.t_down,
+                         router_bias=a.get("router_bias"))
+
+
+def run_layer(qm, rl, x, T):
+    xb = qm.DBuf.from_array(x)
+    ob = qm.DBuf(4 * T * rl.n_embd)
+    qm.moe_ffn_dev(rl.c, xb.ptr, ob.ptr, T)
+    return ob.download(np.float32).reshape(T, rl.n_embd)
+
+
+def check_layer(qm, orc, rl, hl, x, T):
+    N, F, E, K = hl.n_embd, hl.n_ff, hl.n_expert, hl.n_used
+    got = run_layer(qm, rl, x, T)
+    st = qm.moe_last_stage(E, K, F)
+    # stage checks on token 0
+    x0 = x[:N]
+    sel_o, w_o, logits_o = orc.moe_route(hl, x0)
+    assert max_rel_err(st["logits"], logits_o) < TOL
+    if route_margin(logits_o, K) > TIE:
+        assert list(st["sel"]) == list(sel_o)
+        assert np.allclose(st["w"], w_o, rtol=1e-5, atol=1e-7)
+    xq, xd, xs = orc.q8k_quant(x0)
+    assert abs(st["gs"] - orc.moe_shared_gate(hl.gate_inp_shexp, xq, xd, N)) < 1e-6
+    gb = hl.gate_exps.size // E
+    for k in range(K):
+        e = int(st["sel"][k])
+        h = orc.moe_expert_h(hl.gate_exps[e * gb:(e + 1) * gb], hl.up_exps[e * gb:(e + 1) * gb],
+                             N, F, xq, xd, xs)
+        assert max_rel_err(st["h"][k], h) < TOL
+    hsh = orc.moe_expert_h(hl.gate_shexp, hl.up_shexp, N, F, xq, xd, xs)
+    assert max_rel_err(st["h"][K], hsh) < TOL
+    # full outputs, per token; near-tie tokens are run with the GPU routing
+    ref = orc.moe_ffn(hl, x, T)
+    compared = 0
+    for t in range(T):
+        _, _, lg = orc.moe_route(hl, x[t * N:(t + 1) * N])
+        if route_margin(lg, K) > TIE:
+            assert max_rel_err(got[t], ref[t]) < TOL, f"token {t}"
+            compared += 1
+    assert compared >= max(1, T - 1)
+    return got
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(n_embd=512, n_ff=256, n_expert=16, n_used=4, t_down=14),
+    dict(n_embd=256, n_ff=512, n_expert=12, n_used=8, t_down=12),
+    dict(n_embd=1024, n_ff=1024, n_expert=64, n_used=6, t_down=14),
+    dict(n_embd=2048, n_ff=512, n_expert=32, n_used=8, t_down=12),
+])
+def test_moe_layer_small_shapes(qm, orc, cfg):
+    hl = make_host_layer(orc, seed=11, **cfg)
+    rl = qm.ResidentLayer.from_host(hl)
+    for T in (1, 3):
+        x = orc.fill_normal(100 + T, T * cfg["n_embd"], 0.0, 1.0)
+        check_layer(qm, orc, rl, hl, x, T)
+    rl.close()
+
+
+@pytest.mark.parametrize("t_down", [14, 12])
+def test_moe_layer_qwen35moe_shape(qm, orc, t_down):
+    """C3: hidden 2048, 256 experts, top-8, expert ff 512, shared expert,
+    Q4_K gate/up, Q6_K (or Q4_K) down; weights generated in HBM."""
+    rl = qm.ResidentLayer(seed=3, layer=0, t_down=t_down)
+    hl = host_of(orc, rl)
+    x = orc.fill_normal(5, 2048, 0.0, 1.0)
+    check_layer(qm, orc, rl, hl, x, 1)
+    x4 = orc.fill_normal(6, 4 * 2048, 0.0, 1.0)
+    check_layer(qm, orc, rl, hl, x4, 4)
+    rl.close()
+
+
+def test_moe_layer_prefill_skewed_router(qm, orc):
+    """C5 routing: router logits skewed by a seeded per-expert bias ~N(0,1)."""
+    rl = qm.ResidentLayer(seed=9, layer=0, router_bias_std=1.0)
+    hl = host_of(orc, rl)
+    x = orc.fill_normal(15, 16 * 2048, 0.0, 1.0)
+    check_layer(qm, orc, rl, hl, x, 16)
+    rl.close()
+
+
+def test_moe_stack_small(qm, orc):
+    cfg = dict(n_embd=512, n_ff=256, n_expert=16, n_used=4)
+    hls = [make_host_layer(orc, seed=60 + i, **cfg) for i in range(4)]
+    rls = [qm.ResidentLayer.from_host(h) for h in hls]
+    n_tok = 3
+    x = orc.fill_normal(21, n_tok * 512, 0.0, 1.0)
+    xb = qm.DBuf.from_array(x)
+    qm.moe_stack_dev([r.c for r in rls], xb.ptr, n_tok)
+    got = xb.download(np.float32).reshape(n_tok, 512)
+    for t in range(n_tok):
+        ref = orc.moe_stack(hls, x[t * 512:(t + 1) * 512])
+        assert max_rel_err(got[t], ref) < TOL
+
+
+def test_moe_stack_qwen35moe_shape(qm, orc):
+    rls = [qm.ResidentLayer(seed=77, layer=l) for l in range(2)]
+    hls = [host_of(orc, r) for r in rls]
+    x = orc.fill_normal(31, 2 * 2048, 0.0, 1.0)
+    xb = qm.DBuf.from_array(x)
+    qm.moe_stack_dev([r.c for r in rls], xb.ptr, 2)
+    got = xb.download(np.float32).reshape(2, 2048)
+    for t in range(2):
+        ref = orc.moe_stack(hls, x[t * 2048:(t + 1) * 2048])
+        assert max_rel_err(got[t], ref) < TOL
