@@ -133,9 +133,9 @@ def main() -> int:
         log("non-finite output")
         return 1
 
-    # dominant kernel, timed with HIP events on the library stream over one
-    # extra step (the per-kernel events perturb the step total, so this pass
-    # is separate from the timed steps above)
+    # per-kernel launch durations, HIP events on the library stream (the
+    # stream every kernel runs on) around each launch, over one extra step:
+    # per-launch events perturb the step total, so this pass is separate
     qmag.prof_enable(True)
     step()
     qmag.sync()
@@ -143,12 +143,24 @@ def main() -> int:
     qmag.prof_enable(False)
     log("per-kernel: " + ", ".join(f"{k}={n} launches {t / max(n, 1) * 1e3:.2f} us"
                                    for k, (n, t) in prof.items() if n))
-    n_g, t_g = prof["gateup"]
-    gu_us = t_g / n_g * 1e3
-    roofline = {"bound": "hbm", "kernel": "gateup_kernel<8> (9 experts x 512 Q4_K row pairs)",
-                "achieved": GATEUP_LAUNCH_BYTES / (gu_us * 1e-6) / 1e9, "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s", "traffic": None, "bytes_per_launch": GATEUP_LAUNCH_BYTES,
-                "avg_launch_us": gu_us}
+    dom = max(prof, key=lambda k: prof[k][1])
+    n_d, t_d = prof[dom]
+    if dom == "fused":
+        # one launch = one token through all 40 layers; the timed-region
+        # average (events bracketing all launches) includes launch gaps
+        kname = "moe_decode_kernel<Q6_K> (persistent; one token x 40 layers per launch)"
+        bytes_launch = TOKEN_BYTES
+        avg_us = ms / (args.steps * args.tokens) * 1e3
+    else:
+        kname = {"gateup": "gateup_kernel<8>", "down": "down_kernel<2,Q6_K,Q6_K>",
+                 "router": "router_kernel", "topk": "topk_kernel", "hquant": "q8k_quant_kernel"}[dom]
+        bytes_launch = {"gateup": GATEUP_LAUNCH_BYTES, "down": DOWN_LAUNCH_BYTES,
+                        "router": 4 * N_EXPERT * N_EMBD + 4 * N_EMBD}.get(dom, 0)
+        avg_us = t_d / n_d * 1e3
+    roofline = {"bound": "hbm", "kernel": kname,
+                "achieved": bytes_launch / (avg_us * 1e-6) / 1e9, "peak": HBM_PEAK / 1e9,
+                "unit": "GB/s", "traffic": None, "bytes_per_launch": bytes_launch,
+                "avg_launch_us": avg_us, "avg_launch_us_event_pairs": t_d / n_d * 1e3}
     roofline["frac"] = roofline["achieved"] / roofline["peak"]
 
     cpu = None

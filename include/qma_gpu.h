@@ -75,6 +75,9 @@ int qmag_h2d(void *dst, const void *src, size_t bytes);      /* synchronous */
 int qmag_d2h(void *dst, const void *src, size_t bytes);      /* synchronous */
 int qmag_d2d(void *dst, const void *src, size_t bytes);      /* stream-ordered */
 int qmag_memset(void *dst, int value, size_t bytes);         /* stream-ordered */
+/* Wait for the library stream; also reports (QMAG_ERR_KERNEL) a grid-wide
+   wait of the fused decode kernel that hit its spin limit since the last
+   call, and re-arms its counters. */
 int qmag_sync(void);
 
 /* Timing on the library stream: record event `slot` (0..63) and read the
@@ -89,6 +92,20 @@ int qmag_event_elapsed(int a, int b, float *ms);
    returns the launch count and summed milliseconds of one id. */
 int qmag_prof_enable(int on);
 int qmag_prof_read(int kernel_id, long *count, double *total_ms);
+
+/* Options.  QMAG_OPT_FUSED (default 1): batch-1 MoE decode of the qwen35moe
+   shape (n_embd 2048, n_ff 512, n_used <= 8, equal down types) runs as one
+   persistent cooperative kernel per token; 0 selects the per-stage launch
+   sequence (same results within the fp32 tolerance). */
+#define QMAG_OPT_FUSED 1
+/* QMAG_OPT_TRACE (default 0): the fused decode kernel records, per
+   workgroup and layer, 8 phase timestamps of the 100 MHz device real-time
+   counter (layer start, after hop A, router done, after hop B, gate/up
+   start, gate/up done, after hop C, down done); qmag_trace_read copies the
+   last launch's [512][n_layer][8] uint64 array to the host. */
+#define QMAG_OPT_TRACE 2
+int qmag_set_option(int option, int value);
+int qmag_trace_read(void *dst, size_t bytes);
 
 /* ------------------------------------------------------------------------ */
 /* Device entries                                                            */

@@ -110,6 +110,24 @@ __device__ __forceinline__ float group_min(float v)
     return v;
 }
 
+template <int W>
+__device__ __forceinline__ int group_min_i(int v)
+{
+    if constexpr (W >= 2) v = min(v, dpp_i<DPP_XOR1>(v));
+    if constexpr (W >= 4) v = min(v, dpp_i<DPP_XOR2>(v));
+    if constexpr (W >= 8) v = min(v, dpp_i<DPP_HALF_MIRROR>(v));
+    if constexpr (W >= 16) v = min(v, dpp_i<DPP_MIRROR>(v));
+    if constexpr (W >= 32) {
+        auto p = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = min((int)p[0], (int)p[1]);
+    }
+    if constexpr (W >= 64) {
+        auto p = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = min((int)p[0], (int)p[1]);
+    }
+    return v;
+}
+
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
 // --------------------------------------------------------------- loads ----

@@ -60,4 +60,15 @@ int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const fl
             hipStream_t s);
 int moe_check_layer(const qmag_moe_layer *L);
 
+// persistent single-launch decode (qmag_fused.hip)
+bool fused_eligible(const qmag_moe_layer *L, int n_layer);
+int fused_launch(const qmag_moe_layer *L, int n_layer, float *x, float *out, hipStream_t s);
+int fused_status();
+int fused_trace_read(void *dst, size_t bytes);
+int fused_last_stage(const float **logits, const int **sel, const float **w, const float **gs,
+                     const float **h);
+
+// library options (qmag_set_option)
+int option(int id);
+
 }  // namespace qmag

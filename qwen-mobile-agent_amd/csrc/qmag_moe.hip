@@ -440,10 +440,20 @@ int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const fl
 
 using namespace qmag;
 
+static bool g_last_fused = false;
+
 extern "C" int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *out, int T)
 {
     int st = require_ready();
     if (st) return st;
+    st = moe_check_layer(L);
+    if (st) return st;
+    if (T == 1 && option(QMAG_OPT_FUSED) && fused_eligible(L, 1)) {
+        if (!x || !out) return fail(QMAG_ERR_ARG, "moe: null x/out");
+        g_last_fused = true;
+        return fused_launch(L, 1, (float *)x, out, ctx().stream);
+    }
+    g_last_fused = false;
     return moe_ffn(L, x, out, T, nullptr, ctx().stream);
 }
 
@@ -455,8 +465,18 @@ extern "C" int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, flo
     for (int l = 0; l < n_layer; l++) {
         st = moe_check_layer(&layers[l]);
         if (st) return st;
+        if (layers[l].n_embd != layers[0].n_embd) return fail(QMAG_ERR_ARG, "moe_stack: n_embd differs");
     }
     const int N = layers[0].n_embd;
+    if (option(QMAG_OPT_FUSED) && fused_eligible(layers, n_layer)) {
+        g_last_fused = true;
+        for (int t = 0; t < n_tok; t++) {
+            st = fused_launch(layers, n_layer, x + (size_t)t * N, nullptr, ctx().stream);
+            if (st) return st;
+        }
+        return QMAG_OK;
+    }
+    g_last_fused = false;
     for (int t = 0; t < n_tok; t++) {
         float *xt = x + (size_t)t * N;
         for (int l = 0; l < n_layer; l++) {
@@ -470,6 +490,7 @@ extern "C" int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, flo
 extern "C" int qmag_moe_last_stage(const float **logits, const int **sel, const float **w,
                                    const float **gs, const float **h)
 {
+    if (g_last_fused) return fused_last_stage(logits, sel, w, gs, h);
     if (!g_last.logits) return fail(QMAG_ERR_ARG, "no MoE call yet");
     if (logits) *logits = g_last.logits;
     if (sel) *sel = g_last.sel;

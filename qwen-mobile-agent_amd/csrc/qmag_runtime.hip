@@ -20,6 +20,15 @@ static size_t g_ws_cap[WS_COUNT] = {};
 
 Ctx &ctx() { return g_ctx; }
 
+static int g_opt_fused = 1;
+static int g_opt_trace = 0;
+int option(int id)
+{
+    if (id == QMAG_OPT_FUSED) return g_opt_fused;
+    if (id == QMAG_OPT_TRACE) return g_opt_trace;
+    return 0;
+}
+
 int fail(int code, const char *fmt, ...)
 {
     va_list ap;
@@ -252,7 +261,27 @@ int qmag_sync(void)
     int st = require_ready();
     if (st) return st;
     QMAG_HIP(hipStreamSynchronize(g_ctx.stream));
-    return QMAG_OK;
+    return fused_status();
+}
+
+int qmag_set_option(int opt, int value)
+{
+    if (opt == QMAG_OPT_FUSED) {
+        g_opt_fused = value != 0;
+        return QMAG_OK;
+    }
+    if (opt == QMAG_OPT_TRACE) {
+        g_opt_trace = value != 0;
+        return QMAG_OK;
+    }
+    return fail(QMAG_ERR_ARG, "unknown option %d", opt);
+}
+
+int qmag_trace_read(void *dst, size_t bytes)
+{
+    int st = require_ready();
+    if (st) return st;
+    return fused_trace_read(dst, bytes);
 }
 
 int qmag_event_record(int slot)

@@ -42,6 +42,8 @@ SIGNATURES = {
     "qmag_event_elapsed": (C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "qmag_prof_enable": (C.c_int, [C.c_int]),
     "qmag_prof_read": (C.c_int, [C.c_int, C.POINTER(C.c_long), C.POINTER(C.c_double)]),
+    "qmag_set_option": (C.c_int, [C.c_int, C.c_int]),
+    "qmag_trace_read": (C.c_int, [P, C.c_size_t]),
     "qmag_q8k_quant_dev": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
     "qmag_matmul_q8k_dev": (C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_matmul_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
@@ -93,6 +95,31 @@ def device_info():
 
 def sync() -> None:
     check(lib().qmag_sync())
+
+
+OPT_FUSED = 1
+
+
+def set_fused(on: bool) -> None:
+    """Select the persistent single-launch decode kernel (default) or the
+    per-stage launch sequence for batch-1 MoE decode."""
+    check(lib().qmag_set_option(OPT_FUSED, 1 if on else 0))
+
+
+OPT_TRACE = 2
+TRACE_PHASES = ("start", "hopA", "router", "hopB", "gu_start", "gu_done", "hopC", "down_done")
+
+
+def set_trace(on: bool) -> None:
+    check(lib().qmag_set_option(OPT_TRACE, 1 if on else 0))
+
+
+def trace_read(n_layer: int) -> np.ndarray:
+    """Phase timestamps of the last fused launch: uint64 [512][n_layer][8],
+    device real-time counter at 100 MHz."""
+    out = np.empty((512, n_layer, 8), dtype=np.uint64)
+    check(lib().qmag_trace_read(out.ctypes.data_as(P), out.nbytes))
+    return out
 
 
 class DBuf:

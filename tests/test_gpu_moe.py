@@ -22,6 +22,8 @@ def route_margin(logits, n_used):
     p = np.exp(lg - lg.max())
     p /= p.sum()
     s = np.sort(p)[::-1]
+    if n_used >= s.size:          # every expert is selected: no boundary to flip
+        return np.inf
     return (s[n_used - 1] - s[n_used]) / s[n_used - 1]
 
 
@@ -88,17 +90,57 @@ def test_moe_layer_small_shapes(qm, orc, cfg):
     rl.close()
 
 
+@pytest.fixture(params=["fused", "sequence"])
+def decode_path(request, qm):
+    """Batch-1 decode runs as the persistent fused kernel or as the
+    per-stage launch sequence; both must meet the same bar."""
+    qm.set_fused(request.param == "fused")
+    yield request.param
+    qm.set_fused(True)
+
+
 @pytest.mark.parametrize("t_down", [14, 12])
-def test_moe_layer_qwen35moe_shape(qm, orc, t_down):
+def test_moe_layer_qwen35moe_shape(qm, orc, t_down, decode_path):
     """C3: hidden 2048, 256 experts, top-8, expert ff 512, shared expert,
     Q4_K gate/up, Q6_K (or Q4_K) down; weights generated in HBM."""
     rl = qm.ResidentLayer(seed=3, layer=0, t_down=t_down)
     hl = host_of(orc, rl)
-    x = orc.fill_normal(5, 2048, 0.0, 1.0)
-    check_layer(qm, orc, rl, hl, x, 1)
+    for s in (5, 6, 7):
+        x = orc.fill_normal(s, 2048, 0.0, 1.0)
+        check_layer(qm, orc, rl, hl, x, 1)
     x4 = orc.fill_normal(6, 4 * 2048, 0.0, 1.0)
     check_layer(qm, orc, rl, hl, x4, 4)
     rl.close()
+
+
+@pytest.mark.parametrize("n_used,n_expert", [(1, 256), (6, 40), (8, 8)])
+def test_moe_layer_fused_small_routing(qm, orc, n_used, n_expert):
+    """The fused kernel with fewer experts / fewer routed slots than the
+    qwen35moe defaults (hidden 2048 and ff 512 kept)."""
+    hl = make_host_layer(orc, seed=23, n_embd=2048, n_ff=512, n_expert=n_expert, n_used=n_used)
+    rl = qm.ResidentLayer.from_host(hl)
+    x = orc.fill_normal(8, 2048, 0.0, 1.0)
+    check_layer(qm, orc, rl, hl, x, 1)
+    rl.close()
+
+
+def test_moe_decode_paths_agree_40_layers(qm, orc):
+    """40 layers x 3 tokens: fused kernel vs launch sequence (independent
+    kernels), same resident weights."""
+    rls = [qm.ResidentLayer(seed=404, layer=l) for l in range(40)]
+    x = orc.fill_normal(41, 3 * 2048, 0.0, 1.0)
+    outs = []
+    for fused in (True, False):
+        qm.set_fused(fused)
+        xb = qm.DBuf.from_array(x)
+        qm.moe_stack_dev([r.c for r in rls], xb.ptr, 3)
+        qm.sync()
+        outs.append(xb.download(np.float32).reshape(3, 2048))
+    qm.set_fused(True)
+    for t in range(3):
+        assert max_rel_err(outs[0][t], outs[1][t]) < TOL
+    for r in rls:
+        r.close()
 
 
 def test_moe_layer_prefill_skewed_router(qm, orc):
@@ -124,7 +166,7 @@ def test_moe_stack_small(qm, orc):
         assert max_rel_err(got[t], ref) < TOL
 
 
-def test_moe_stack_qwen35moe_shape(qm, orc):
+def test_moe_stack_qwen35moe_shape(qm, orc, decode_path):
     rls = [qm.ResidentLayer(seed=77, layer=l) for l in range(2)]
     hls = [host_of(orc, r) for r in rls]
     x = orc.fill_normal(31, 2 * 2048, 0.0, 1.0)
