@@ -36,6 +36,11 @@ TOKEN_BYTES = N_LAYER * LAYER_TOKEN_BYTES                      # 818,544,640
 GATEUP_LAUNCH_BYTES = (N_USED + 1) * 2 * N_FF * Q4K_ROW + N_EMBD + 32 + 256 + (N_USED + 1) * N_FF * 4
 DOWN_LAUNCH_BYTES = (N_USED + 1) * N_EMBD * Q6K_ROW + (N_USED + 1) * (N_FF + 8 + 64) + 4 * N_EMBD * 2
 METRIC = "MoE FFN decode tokens/s + achieved HBM GB/s (% of peak), Q4_K/Q6_K, 1 GPU"
+# HBM bytes per launch of the fused decode kernel as built from this tree,
+# from two rocprofv3 counter passes over bench.py (FETCH_SIZE x 2.000 +
+# WRITE_SIZE x 1.000, the factors read off a 1 GiB copy kernel in the same
+# runs); re-measured whenever the kernel changes.
+FUSED_TRAFFIC_BYTES = 947.6e6
 
 
 def log(msg: str) -> None:
@@ -90,6 +95,13 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--tokens", type=int, default=N_TOK)
+    ap.add_argument("--decode", choices=("fused", "sequence"), default="fused",
+                    help="persistent single-launch decode (default) or the per-stage launch sequence")
+    ap.add_argument("--launch", choices=("coop", "plain"), default="plain",
+                    help="fused kernel: ordinary launch (default) or cooperative launch")
+    ap.add_argument("--probe-copy-mb", type=int, default=0,
+                    help="after the run, one device-to-device copy of this many MiB between two "
+                         "fresh buffers: a copy kernel of known size for scaling HBM counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -98,6 +110,8 @@ def main() -> int:
         return 2
 
     qmag.init(0)
+    qmag.set_fused(args.decode == "fused")
+    qmag.set_coop(args.launch == "coop")
     info = qmag.device_info()
     log(f"device {info}")
     t0 = time.perf_counter()
@@ -159,9 +173,19 @@ def main() -> int:
         avg_us = t_d / n_d * 1e3
     roofline = {"bound": "hbm", "kernel": kname,
                 "achieved": bytes_launch / (avg_us * 1e-6) / 1e9, "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s", "traffic": None, "bytes_per_launch": bytes_launch,
+                "unit": "GB/s", "traffic": FUSED_TRAFFIC_BYTES if dom == "fused" else None,
+                "bytes_per_launch": bytes_launch,
                 "avg_launch_us": avg_us, "avg_launch_us_event_pairs": t_d / n_d * 1e3}
     roofline["frac"] = roofline["achieved"] / roofline["peak"]
+
+    if args.probe_copy_mb > 0:
+        nb = args.probe_copy_mb << 20
+        src, dst = qmag.DBuf(nb), qmag.DBuf(nb)
+        qmag.synth_normal(7, nb // 4, 0.0, 1.0, src.ptr)
+        qmag.check(qmag.lib().qmag_d2d(dst.ptr, src.ptr, nb))
+        qmag.sync()
+        del src, dst
+        log(f"probe copy of {args.probe_copy_mb} MiB done")
 
     cpu = None
     if not args.no_cpu:
@@ -178,7 +202,8 @@ def main() -> int:
                                "sequential at batch 1, all experts resident",
                    "n_layer": N_LAYER, "tokens_per_step": args.tokens, "n_embd": N_EMBD,
                    "n_expert": N_EXPERT, "n_used": N_USED, "n_ff": N_FF,
-                   "gate_up": "Q4_K", "down": "Q6_K", "parallelism": "single GPU"},
+                   "gate_up": "Q4_K", "down": "Q6_K", "parallelism": "single GPU",
+                   "decode": args.decode, "launch": args.launch},
         "hbm_gbps": gbps, "hbm_frac_of_peak": gbps * 1e9 / HBM_PEAK,
         "bytes_per_token": TOKEN_BYTES,
         "roofline": roofline, "cpu_baseline": cpu,

@@ -104,6 +104,15 @@ int qmag_prof_read(int kernel_id, long *count, double *total_ms);
    start, gate/up done, after hop C, down done); qmag_trace_read copies the
    last launch's [512][n_layer][8] uint64 array to the host. */
 #define QMAG_OPT_TRACE 2
+/* QMAG_OPT_COOP (default 0): 1 launches the fused decode kernel with
+   hipLaunchCooperativeKernel (co-residency of its 512 workgroups guaranteed
+   by the runtime); 0 launches it as an ordinary kernel after the occupancy
+   check that makes it eligible (two workgroups per CU fit, so all are
+   resident when the device is otherwise idle; a workgroup that were not
+   would make the others exhaust their bounded waits, reported as
+   QMAG_ERR_KERNEL by qmag_sync, never a hang).  The ordinary launch is the
+   default: equally fast, and visible to rocprofv3's kernel tracing. */
+#define QMAG_OPT_COOP 3
 int qmag_set_option(int option, int value);
 int qmag_trace_read(void *dst, size_t bytes);
 

@@ -699,7 +699,10 @@ int fused_launch(const qmag_moe_layer *L, int n_layer, float *x, float *out, hip
                         ? (const void *)fused::moe_decode_kernel<QMAG_TYPE_Q6_K>
                         : (const void *)fused::moe_decode_kernel<QMAG_TYPE_Q4_K>;
     prof_begin(PROF_FUSED, s);
-    QMAG_HIP(hipLaunchCooperativeKernel(k, dim3(fused::WGS), dim3(256), args, 0, s));
+    if (option(QMAG_OPT_COOP))
+        QMAG_HIP(hipLaunchCooperativeKernel(k, dim3(fused::WGS), dim3(256), args, 0, s));
+    else       // fused_eligible checked that every workgroup fits at once
+        QMAG_HIP(hipLaunchKernel(k, dim3(fused::WGS), dim3(256), args, 0, s));
     prof_end(PROF_FUSED, s);
     g_epoch++;
     return QMAG_OK;

@@ -22,10 +22,12 @@ Ctx &ctx() { return g_ctx; }
 
 static int g_opt_fused = 1;
 static int g_opt_trace = 0;
+static int g_opt_coop = 0;
 int option(int id)
 {
     if (id == QMAG_OPT_FUSED) return g_opt_fused;
     if (id == QMAG_OPT_TRACE) return g_opt_trace;
+    if (id == QMAG_OPT_COOP) return g_opt_coop;
     return 0;
 }
 
@@ -272,6 +274,10 @@ int qmag_set_option(int opt, int value)
     }
     if (opt == QMAG_OPT_TRACE) {
         g_opt_trace = value != 0;
+        return QMAG_OK;
+    }
+    if (opt == QMAG_OPT_COOP) {
+        g_opt_coop = value != 0;
         return QMAG_OK;
     }
     return fail(QMAG_ERR_ARG, "unknown option %d", opt);

@@ -114,6 +114,15 @@ def set_trace(on: bool) -> None:
     check(lib().qmag_set_option(OPT_TRACE, 1 if on else 0))
 
 
+OPT_COOP = 3
+
+
+def set_coop(on: bool) -> None:
+    """Launch the fused decode kernel cooperatively, or (default) as an
+    ordinary kernel after the occupancy check that makes it eligible."""
+    check(lib().qmag_set_option(OPT_COOP, 1 if on else 0))
+
+
 def trace_read(n_layer: int) -> np.ndarray:
     """Phase timestamps of the last fused launch: uint64 [512][n_layer][8],
     device real-time counter at 100 MHz."""
