@@ -87,6 +87,82 @@ def cpu_baseline(layers, seconds: float, n_layer_sample: int = 8):
                       f"layers; nproc={os.cpu_count()}, cpu={cpu}"}
 
 
+def matvec_bytes(n_in: int, n_out: int, wtype: int) -> int:
+    """Algorithmic bytes of one matmul-seam call at T = 1: weights, the
+    fp32 input, its Q8_K form and the fp32 output."""
+    rb = n_in // 256 * (144 if wtype == 12 else 210)
+    return rb * n_out + 4 * n_in + (n_in + 4 * (n_in // 256) + 2 * (n_in // 16)) + 4 * n_out
+
+
+def aux_matvec(name: str, n_in: int, n_out: int, wtype: int, copies: int, iters: int) -> dict:
+    """Configs C1/C2: the matmul seam (Q8_K of x, then the matvec) at T = 1,
+    rotating over `copies` distinct weight matrices so the working set
+    exceeds the 256 MB last-level cache."""
+    rb = n_in // 256 * (144 if wtype == 12 else 210)
+    Ws = [qmag.DBuf(rb * n_out) for _ in range(copies)]
+    for i, w in enumerate(Ws):
+        qmag.synth_weights(0xC100 + i, n_in * n_out, 0.02, wtype, w.ptr)
+    x = qmag.DBuf(4 * n_in)
+    qmag.synth_normal(0xC1, n_in, 0.0, 1.0, x.ptr)
+    out = qmag.DBuf(4 * n_out)
+    for w in Ws:
+        qmag.matmul_dev(x, w, n_in, n_out, 1, wtype, out)
+    qmag.sync()
+    timer = qmag.Timer(2, 3)
+    timer.start()
+    for _ in range(iters):
+        for w in Ws:
+            qmag.matmul_dev(x, w, n_in, n_out, 1, wtype, out)
+    ms = timer.stop_ms()
+    calls = iters * copies
+    qmag.prof_enable(True)
+    for w in Ws:
+        qmag.matmul_dev(x, w, n_in, n_out, 1, wtype, out)
+    qmag.sync()
+    n_mv, t_mv = qmag.prof_read("matvec")
+    n_q, t_q = qmag.prof_read("q8k")
+    qmag.prof_enable(False)
+    for w in Ws:
+        w.close()
+    nbytes = matvec_bytes(n_in, n_out, wtype)
+    call_us = ms * 1e3 / calls
+    mv_us = t_mv * 1e3 / max(n_mv, 1)
+    res = {"config": name, "bytes_per_call": nbytes, "us_per_call": call_us,
+           "gbps_per_call": nbytes / (call_us * 1e-6) / 1e9,
+           "matvec_kernel_us": mv_us, "q8k_kernel_us": t_q * 1e3 / max(n_q, 1),
+           "matvec_kernel_gbps": rb * n_out / (mv_us * 1e-6) / 1e9,
+           "weight_copies": copies}
+    res["matvec_kernel_frac_of_peak"] = res["matvec_kernel_gbps"] * 1e9 / HBM_PEAK
+    log(f"{name}: {call_us:.2f} us/call ({res['gbps_per_call']:.0f} GB/s incl. launches), "
+        f"matvec kernel {mv_us:.2f} us = {res['matvec_kernel_gbps']:.0f} GB/s")
+    return res
+
+
+def aux_layer(cl, iters: int) -> dict:
+    """Config C3: one MoE layer per call (T = 1, qmag_moe_ffn_dev), rotating
+    over the 40 resident layers."""
+    x = qmag.DBuf(4 * N_EMBD)
+    out = qmag.DBuf(4 * N_EMBD)
+    qmag.synth_normal(0xC3, N_EMBD, 0.0, 1.0, x.ptr)
+    for c in cl:
+        qmag.moe_ffn_dev(c, x.ptr, out.ptr, 1)
+    qmag.sync()
+    timer = qmag.Timer(2, 3)
+    timer.start()
+    for _ in range(iters):
+        for c in cl:
+            qmag.moe_ffn_dev(c, x.ptr, out.ptr, 1)
+    ms = timer.stop_ms()
+    us = ms * 1e3 / (iters * len(cl))
+    res = {"config": "C3: one qwen35moe MoE FFN layer, batch-1 decode, one call per layer "
+                     "rotating over 40 resident layers",
+           "bytes_per_call": LAYER_TOKEN_BYTES, "us_per_call": us,
+           "gbps": LAYER_TOKEN_BYTES / (us * 1e-6) / 1e9}
+    res["frac_of_peak"] = res["gbps"] * 1e9 / HBM_PEAK
+    log(f"C3 layer: {us:.2f} us/call, {res['gbps']:.0f} GB/s")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,6 +178,8 @@ def main() -> int:
     ap.add_argument("--probe-copy-mb", type=int, default=0,
                     help="after the run, one device-to-device copy of this many MiB between two "
                          "fresh buffers: a copy kernel of known size for scaling HBM counters")
+    ap.add_argument("--no-aux", action="store_true",
+                    help="skip the C1/C2 matvec and C3 single-layer measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -187,6 +265,12 @@ def main() -> int:
         del src, dst
         log(f"probe copy of {args.probe_copy_mb} MiB done")
 
+    aux = None
+    if not args.no_aux:
+        aux = {"c1": aux_matvec("C1: Q4_K matvec 2048x2048, matmul seam, T=1", 2048, 2048, 12, 128, 20),
+               "c2": aux_matvec("C2: Q6_K LM head 151936x2048, matmul seam, T=1", 2048, 151936, 14, 2, 20),
+               "c3": aux_layer(cl, 5)}
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -208,6 +292,7 @@ def main() -> int:
         "bytes_per_token": TOKEN_BYTES,
         "roofline": roofline, "cpu_baseline": cpu,
         "per_kernel_us": {k: t / n * 1e3 for k, (n, t) in prof.items() if n},
+        "aux": aux,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -88,7 +88,8 @@ int qmag_event_elapsed(int a, int b, float *ms);
 /* Per-kernel timing (the QMA_TIMING role, nn.c:219-259, on the GPU): while
    enabled, every kernel the MoE entries launch is bracketed by HIP events on
    the library stream.  Kernel ids: 0 router, 1 top-k/Q8_K(x), 2 gate/up,
-   3 Q8_K(h), 4 down+combine, 5 fused decode.  qmag_prof_read synchronises and
+   3 Q8_K(h), 4 down+combine, 5 fused decode, 6 matvec (matmul entries),
+   7 Q8_K quantisation (every launch of it).  qmag_prof_read synchronises and
    returns the launch count and summed milliseconds of one id. */
 int qmag_prof_enable(int on);
 int qmag_prof_read(int kernel_id, long *count, double *total_ms);

@@ -46,7 +46,10 @@ enum WsSlot {
 void *workspace(int slot, size_t bytes, int *status);
 
 // ---- per-kernel event timing (qmag_prof_*) ----
-enum ProfId { PROF_ROUTER = 0, PROF_TOPK, PROF_GATEUP, PROF_HQUANT, PROF_DOWN, PROF_FUSED, PROF_COUNT };
+enum ProfId {
+    PROF_ROUTER = 0, PROF_TOPK, PROF_GATEUP, PROF_HQUANT, PROF_DOWN, PROF_FUSED, PROF_MATVEC, PROF_Q8K,
+    PROF_COUNT
+};
 bool prof_on();
 void prof_begin(int id, hipStream_t s);
 void prof_end(int id, hipStream_t s);

@@ -33,7 +33,9 @@ int launch_q8k_quant(const float *x, int nblocks, int8_t *xq, float *xd, int16_t
     if (nblocks <= 0) return QMAG_OK;
     if (!x || !xq || !xd || !xsum) return fail(QMAG_ERR_ARG, "q8k_quant: null pointer");
     const int wgs = (nblocks + 3) / 4;
+    prof_begin(PROF_Q8K, s);
     hipLaunchKernelGGL(q8k_quant_kernel, dim3(wgs), dim3(256), 0, s, x, nblocks, xq, xd, xsum);
+    prof_end(PROF_Q8K, s);
     QMAG_HIP(hipGetLastError());
     return QMAG_OK;
 }
@@ -166,12 +168,14 @@ static int launch_mv_nb(const int8_t *xq, const float *xd, const int16_t *xsum, 
     const long cap = (long)(ctx().n_cu > 0 ? ctx().n_cu : 256) * 32;    // waves
     const long waves = groups < cap ? groups : cap;
     const int wgs = (int)((waves + 3) / 4);
+    prof_begin(PROF_MATVEC, s);
     if (T == 1)
         hipLaunchKernelGGL((matvec_kernel<WT, NB, true>), dim3(wgs), dim3(256), 0, s,
                            (const uint8_t *)W, xq, xd, xsum, out, n_out, T);
     else
         hipLaunchKernelGGL((matvec_kernel<WT, NB, false>), dim3(wgs), dim3(256), 0, s,
                            (const uint8_t *)W, xq, xd, xsum, out, n_out, T);
+    prof_end(PROF_MATVEC, s);
     QMAG_HIP(hipGetLastError());
     return QMAG_OK;
 }

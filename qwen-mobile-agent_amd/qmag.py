@@ -241,7 +241,8 @@ def quantize_dev(x_ptr: int, n: int, wtype: int, out_ptr: int) -> None:
     check(lib().qmag_quantize_dev(x_ptr, n, wtype, out_ptr))
 
 
-PROF_IDS = {"router": 0, "topk": 1, "gateup": 2, "hquant": 3, "down": 4, "fused": 5}
+PROF_IDS = {"router": 0, "topk": 1, "gateup": 2, "hquant": 3, "down": 4, "fused": 5, "matvec": 6,
+            "q8k": 7}
 
 
 def prof_enable(on: bool) -> None:
