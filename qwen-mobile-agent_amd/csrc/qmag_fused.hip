@@ -1,33 +1,43 @@
-// qmag_fused.hip -- one persistent, cooperatively launched kernel that runs
-// the whole qwen35moe MoE FFN decode (batch 1) for a run of layers
-// (src/nn.c:509-707 per layer, residual add of nn.c:2252 between layers).
+// qmag_fused.hip -- one persistent kernel that runs the whole qwen35moe MoE
+// FFN decode (batch 1) for a run of layers (src/nn.c:509-707 per layer, the
+// residual add of nn.c:2252 between layers).
 //
 // Shapes are the engine's compile-time ones (src/qma.h:28, 57-60): hidden
 // 2048, expert ff 512, up to 256 experts, top-k <= 8, plus the shared
-// expert.  512 workgroups x 4 waves = 2048 waves, two workgroups per CU;
-// wave w owns down row w of every layer.
+// expert.  512 workgroups x 4 waves, two workgroups per CU, in two roles:
 //
-// Data flow of one layer, five hand-offs between workgroups:
-//   1  x_l rows             down waves of layer l-1  -> the router workgroups
-//   2  router logits        router waves              -> the collector (wave 0 of wg 0)
-//   3  selection record     collector: top-k ids, renormalised weights and the
-//                           shared-expert gate; with it Q8_K(x_l)  -> every workgroup
-//   4  h = silu(g)*u        gate/up waves             -> 18 quantiser waves
-//   5  Q8_K(h) blocks       quantiser waves           -> every workgroup
-// No counters or cross-workgroup barriers exist.  Every published value is
-// one 64-bit word {32 data bits, 32-bit tag}, written with a single-copy-
-// atomic device-scope store; the tag is epoch*256 + layer + 1 (the epoch
-// counts launches).  A consumer reads words with device-scope atomic loads
-// and accepts a word only when it carries the current tag, so data is its own
-// ready flag and no read-modify-write or cache maintenance is needed.  Bulk
-// data is read once its sentinel words are valid (every word is still
-// validated), so waiting workgroups poll a handful of words, not the bulk.
-// Values all 512 workgroups read are written in 8 replicas 64 KB apart.
+//   core workgroups 0..127 (16 per XCD) each own 16 rows of the hidden state.
+//     They compute the router logits (2 per workgroup, router rows staged in
+//     LDS one layer ahead), Q8_K(x) (workgroups 0..7, one 256-block each,
+//     with that block's share of the shared-expert gate input) and the down
+//     projection + combine + residual of their rows for all 9 slots, with
+//     the down rows fetched into registers as soon as the selection is known.
+//   stream workgroups 128..511 (1536 waves) compute the gate/up row pairs:
+//     slot s < n_used is routed expert sel[s], slot n_used the shared one,
+//     three row pairs per wave; afterwards 18 of their waves quantise one
+//     h block each (a wave's loads complete in order, so pollers are kept
+//     out of the waves that hold prefetches in flight).
 //
-// Weight bytes move as early as they are known: the router row (straight
-// into LDS) at layer start, and right after the selection record the gate/up
-// row pairs and down-row slices of the routed and shared experts, all issued
-// before any is consumed, so the down bytes stream while gate/up computes.
+// Hand-offs of one layer (each a set of tagged words, see below):
+//   x_l rows      core -> core            (2048 words, read by 128 workgroups)
+//   logits        core -> every workgroup (256 words, 8 replicas); every
+//                 workgroup runs the softmax/top-k itself, so the selection
+//                 needs no further hop
+//   Q8_K(x)       core 0..7 -> stream     (656 words, 8 replicas; produced
+//                 together with the logits, off the critical path)
+//   h             stream -> 18 quantiser waves
+//   Q8_K(h)       quantiser -> core       (1458 words, read by 128 workgroups)
+//
+// Every published value is one 64-bit word {32 data bits, 32-bit tag},
+// written with a single-copy-atomic device-scope store; the tag is
+// epoch*256 + layer + 1 (the epoch counts launches, so no buffer is ever
+// cleared between launches).  A consumer reads words with device-scope
+// atomic loads and accepts a word only when it carries the current tag: data
+// is its own ready flag, and no read-modify-write, barrier or cache
+// maintenance is needed.  Each buffer has one slot: a word of layer l+1 is
+// written only after every reader of the layer-l word has consumed it (the
+// dependency chain of the layer passes through every such reader).
+//
 // Every poll is bounded: an exhausted waiter raises an abort flag that all
 // pollers check, so the grid always drains; qmag_sync() reports it.
 #include <string.h>
@@ -40,41 +50,52 @@ namespace fused {
 constexpr int N = 2048, F = 512;
 constexpr int NBE = N / QK_K, NBF = F / QK_K;     // 8, 2
 constexpr int SMAX = 9;                           // 8 routed + shared
-constexpr int WGS = 512, WAVES = WGS * 4;
-constexpr int MAX_RP = (SMAX * F + WAVES - 1) / WAVES;   // gate/up row pairs per wave: 3
+constexpr int WGS = 512;
+constexpr int CORE = 128;                         // core workgroups
+constexpr int CROWS = N / CORE;                   // 16 hidden rows per core workgroup
+constexpr int WROWS = CROWS / 4;                  // 4 per core wave
+constexpr int NLOG = 256 / CORE;                  // 2 router logits per core workgroup
+constexpr int GU_WAVES = (WGS - CORE) * 4;        // 1536 gate/up waves
+constexpr int MAX_RP = (SMAX * F + GU_WAVES - 1) / GU_WAVES;   // 3 row pairs per wave
+constexpr int DN_TASKS = WROWS * SMAX;            // (row, slot) pairs per core wave: 36
+constexpr int DN_ROUNDS = (DN_TASKS + 7) / 8;     // 8 lanes per pair: 5 rounds
 constexpr long SPIN_LIMIT = 1L << 22;
 
-// Q8_K(x): 512 packed xq words, 8 block scales, 128 group sums
-constexpr int XQ_WORDS = N / 4 + NBE + N / 16;    // 648
-constexpr int XQ_D = N / 4, XQ_S = N / 4 + NBE;
-// selection record: 8 expert ids, 8 weights, the shared-expert gate
-constexpr int SEL_WORDS = 17;
-// Q8_K(h): per 256-value block 64 packed words, the scale (the block's
-// sentinel), 16 group sums; block k is quantised by wave 1 of workgroup
-// QWG0 + k*QWG_STEP (odd step: spread over the 8 XCDs, which take
-// workgroups round-robin)
-constexpr int HQ_BLK = 64 + 1 + 16;
-constexpr int HQ_PER_THREAD = (SMAX * NBF * HQ_BLK + 255) / 256;   // 6
-constexpr int QWG0 = 3, QWG_STEP = 29;
-static_assert(QWG0 + QWG_STEP * (SMAX * NBF - 1) < WGS, "quantiser workgroups out of range");
+// Q8_K records are laid out exactly as the LDS copy their readers keep, so a
+// reader copies word i to LDS word i:
+//   Q8_K(x): 512 packed xq words (block b at 64b), 8 scales d, 128 group
+//   sums, 8 partials of the shared-expert gate input (nn.c:452-454)
+constexpr int XR_D = N / 4, XR_S = XR_D + NBE, XR_G = XR_S + N / 16, XR_WORDS = XR_G + NBE;   // 656
+//   Q8_K(h), 2*SMAX blocks: packed words, scales (block k's scale is the
+//   word its readers poll first), group sums
+constexpr int HBLK = SMAX * NBF;                  // 18
+constexpr int HR_D = HBLK * 64, HR_S = HR_D + HBLK, HR_WORDS = HR_S + HBLK * 16;            // 1458
+constexpr int HQ_PAIRS_PER_THREAD = (HR_WORDS / 2 + 255) / 256;   // 3
+static_assert(HR_D % 2 == 0 && HR_S % 2 == 0 && HR_WORDS % 2 == 0, "Q8_K(h) record ranges must be even");
+constexpr int REP = 8;                            // replicas of the widely read records
+// h block k (k < 2*SMAX) is quantised by wave 1 of stream workgroup
+// QWG0 + k*QWG_STEP, after that wave's own gate/up rows (odd step: the
+// quantisers spread over the 8 XCDs, which take workgroups round-robin)
+constexpr int QWG0 = CORE + 3, QWG_STEP = 21;
+static_assert(QWG0 + QWG_STEP * (2 * SMAX - 1) < WGS, "quantiser workgroups out of range");
 
-// The selection record, polled by every workgroup, is written in REP
-// replicas 4 KB apart (workgroup b polls replica b % REP).  The bulk values
-// every workgroup reads (Q8_K(x), Q8_K(h)) get one buffer per layer slot, so
-// a cache line read in one layer is not looked up again until the slot comes
-// round on the next token.
-constexpr int REP = 8, REP_WORDS = 512;
-constexpr int MAXL = 64;                          // layer slots (layer l uses l % MAXL)
-constexpr int XQ_PAD = 656, HQ_PAD = 1472;        // words, multiples of 16 (128 B)
 struct Tagged {
-    unsigned long long sel[REP][REP_WORDS];
-    unsigned long long xq[MAXL][XQ_PAD];
-    unsigned long long hq[MAXL][HQ_PAD];
-    unsigned long long x[N];             // x_l, l >= 1 (read by the router workgroups)
-    unsigned long long logits[256];      // read by the collector
-    unsigned long long h[SMAX * F];      // read by the quantiser waves
+    unsigned long long logits[REP][256];          // logit e at word logit_pos(e)
+    unsigned long long xq[REP][XR_WORDS];
+    unsigned long long x[N];
+    unsigned long long h[SMAX * F];
+    unsigned long long hq[HR_WORDS + 14];         // padded to a multiple of 16 words
 };
-static_assert(XQ_PAD >= XQ_WORDS && HQ_PAD >= SMAX * NBF * HQ_BLK, "slot sizes");
+// word offsets of the arrays (every array starts on a 16-byte boundary)
+constexpr int TW_LOGITS = 0, TW_XQ = TW_LOGITS + REP * 256, TW_X = TW_XQ + REP * XR_WORDS,
+              TW_H = TW_X + N, TW_HQ = TW_H + SMAX * F;
+static_assert(offsetof(Tagged, xq) == 8 * TW_XQ && offsetof(Tagged, x) == 8 * TW_X &&
+              offsetof(Tagged, h) == 8 * TW_H && offsetof(Tagged, hq) == 8 * TW_HQ && XR_WORDS % 2 == 0,
+              "tagged layout");
+// Logits are stored so that the 16-byte pair p of lane l (p = l, l + 64)
+// holds experts l + 64h + 128(p >= 64), h = the half: a lane then reads
+// experts l, l+64, l+128, l+192, the layout the top-k works on.
+__device__ __forceinline__ int logit_pos(int e) { return 2 * ((e & 63) + 64 * (e >> 7)) + ((e >> 6) & 1); }
 
 __device__ __forceinline__ unsigned long long ld64(const unsigned long long *p)
 {
@@ -83,12 +104,6 @@ __device__ __forceinline__ unsigned long long ld64(const unsigned long long *p)
 __device__ __forceinline__ void st64(unsigned long long *p, uint32_t v, uint32_t seq)
 {
     __hip_atomic_store(p, ((unsigned long long)seq << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// p points into replica 0; the word is written in every replica
-__device__ __forceinline__ void st64r(unsigned long long *p, uint32_t v, uint32_t seq)
-{
-#pragma nounroll
-    for (int r = 0; r < REP; r++) st64(p + r * REP_WORDS, v, seq);
 }
 // wait until all of this wave's outstanding memory operations completed
 __device__ __forceinline__ void drain() { __builtin_amdgcn_s_waitcnt(0); }
@@ -128,24 +143,46 @@ __device__ bool poll(const unsigned long long *p, Idx idx, uint32_t seq, uint32_
     return false;
 }
 
-// Bulk read after the sentinels were seen: one pass of ordinary (L2-cached)
-// loads, so the 64 workgroups of an XCD share one fetch from memory; words
-// with a stale tag (a stale cache line) are then polled device-coherently.
-template <int CNT, typename Idx>
-__device__ bool read_bulk(const unsigned long long *p, Idx idx, uint32_t seq, uint32_t (&val)[CNT],
-                          int *abort_flag)
+// Bulk reads take two tagged words per 16-byte load: a buffer load with the
+// same device-coherent cache policy (sc1) as the 8-byte atomic loads.  Each
+// 8-byte half is single-copy atomic and checked against its own tag, so the
+// pair needs no atomicity as a whole; 16-byte loads halve the requests,
+// which is what bounds a workgroup's bulk read rate.
+constexpr int CPOL_SC1 = 16;
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+// One wave reads CNT word pairs per lane.  code(k) = pair index * 4 + need
+// (need: bit 0 the low word, bit 1 the high word must carry seq), or -1 for
+// no pair.  Word offsets are relative to the resource base; the low 32 bits
+// of the needed words land in val[k][0..1].
+template <int CNT, typename Code>
+__device__ bool pollq(Rsrc rs, int base_word, Code code, uint32_t seq, uint32_t (&val)[CNT][2],
+                      int *abort_flag)
 {
-    bool fresh = true;
+    uint32_t pending = 0;
 #pragma unroll
-    for (int k = 0; k < CNT; k++) {
-        if (idx(k) >= 0) {
-            const unsigned long long w = p[idx(k)];
-            val[k] = (uint32_t)w;
-            fresh = fresh && (uint32_t)(w >> 32) == seq;
+    for (int k = 0; k < CNT; k++)
+        if (code(k) >= 0) pending |= 1u << k;
+    for (long it = 0; it < SPIN_LIMIT; it++) {
+#pragma unroll
+        for (int k = 0; k < CNT; k++) {
+            if (pending & (1u << k)) {
+                const int c = code(k);
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (base_word + 2 * (c >> 2)) * 8, 0, CPOL_SC1);
+                const bool lo = !(c & 1) || v[1] == seq, hi = !(c & 2) || v[3] == seq;
+                if (lo && hi) {
+                    val[k][0] = v[0];
+                    val[k][1] = v[2];
+                    pending &= ~(1u << k);
+                }
+            }
         }
+        if (__all(pending == 0)) return true;
+        if ((it & 31) == 31 && ld_flag(abort_flag) != 0) return false;
+        __builtin_amdgcn_s_sleep(2);
     }
-    if (__all(fresh)) return true;
-    return poll<CNT>(p, idx, seq, val, abort_flag);
+    __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return false;
 }
 
 // workgroup-wide AND of one flag per wave (slot: a distinct LDS row per call site)
@@ -156,7 +193,7 @@ __device__ __forceinline__ bool wg_all(bool ok, int (*s_vote)[4], int slot)
     return (s_vote[slot][0] & s_vote[slot][1] & s_vote[slot][2] & s_vote[slot][3]) != 0;
 }
 
-// ---- down-projection task (row r of one expert, 8 tasks per 512-wide row)
+// ---- down-projection task: 8 lanes per (row, slot), lane q of the 8
 template <int TD>
 struct DRaw;
 template <>
@@ -188,10 +225,11 @@ __device__ __forceinline__ void d_load(DRaw<TD> &d, const uint8_t *slab, int row
     }
 }
 
-// fp32 contribution of task q against one slot's Q8_K(h) held in LDS
+// fp32 contribution of task q against one slot's Q8_K(h) held in LDS; the
+// 8 lanes of a (row, slot) pair sum to the row's dot (blocks in order)
 template <int TD>
 __device__ __forceinline__ float d_dot(const DRaw<TD> &d, const uint32_t *hq, const float *hd,
-                                       const int16_t *hs, int q)
+                                       const int *hs, int q)
 {
     const int ib = q >> 2, sub = q & 3;
     if constexpr (TD == QMAG_TYPE_Q6_K) {
@@ -218,17 +256,20 @@ __device__ __forceinline__ float d_dot(const DRaw<TD> &d, const uint32_t *hq, co
             a.x[4 * k + 3] = w.w;
         }
         a.xd = hd[ib];
-        const int16_t *s = hs + ib * 16 + 4 * sub;
+        const int *s = hs + ib * 16 + 4 * sub;
         a.sx0 = (float)(s[0] + s[1]);
         a.sx1 = (float)(s[2] + s[3]);
         return q4_task(d.hdr, d.q0, d.q1, a, sub);
     }
 }
 
-// softmax over E <= 256 logits (4 per lane of one wave), top-K with strict
-// > and the lowest index winning ties (nn.c:525-536).  Lane k < K receives
-// pick k: its expert id and its weight renormalised over the K picks (the
-// sum taken in pick order, as the reference does).
+// softmax over E <= 256 logits (4 per lane of one wave, expert lane + 64j),
+// then the K largest probabilities in the order nn.c:525-536 picks them:
+// each pick is the maximum of what is left, the lowest index among equal
+// values.  The maximum is one DPP/permlane reduction; the lowest index
+// holding it comes from four ballots and scalar bit scans.  Lane k < K
+// receives pick k: its expert id and its weight renormalised over the K
+// picks (the sum taken in pick order).
 __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, float &my_w)
 {
     const int lane = lane_id();
@@ -246,24 +287,23 @@ __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, floa
     se = group_sum<64>(se);
 #pragma unroll
     for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < E ? p[j] / se : -1.0f;
+    float ws = 0.0f;
     for (int k = 0; k < K; k++) {
         const float m = group_max<64>(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])));
-        int cand = 1 << 30;
-#pragma unroll
-        for (int j = 3; j >= 0; j--)
-            if (p[j] == m) cand = lane + 64 * j;
-        int s = group_min_i<64>(cand);
-        s = s < E ? s : 0;          // NaN logits match nothing: keep the index in range
+        const unsigned long long b0 = __ballot(p[0] == m), b1 = __ballot(p[1] == m), b2 = __ballot(p[2] == m),
+                                 b3 = __ballot(p[3] == m);
+        // NaN probabilities equal nothing: fall back to expert 0, in range
+        const int e = b0 ? __builtin_ctzll(b0) : b1 ? 64 + __builtin_ctzll(b1)
+                    : b2 ? 128 + __builtin_ctzll(b2) : b3 ? 192 + __builtin_ctzll(b3) : 0;
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            if (lane + 64 * j == s) p[j] = -1.0f;
+            if (lane + 64 * j == e) p[j] = -1.0f;
         if (lane == k) {
-            my_sel = s;
+            my_sel = e;
             my_w = m;
         }
+        ws += m;
     }
-    float ws = 0.0f;
-    for (int k = 0; k < K; k++) ws += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), k));
     my_w = my_w / ws;
 }
 
@@ -275,211 +315,303 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                                                             int *abort_flag, unsigned epoch,
                                                             unsigned long long *trace)
 {
-    __shared__ uint4 s_xq[N / 16];
-    __shared__ float s_xd[NBE];
-    __shared__ int16_t s_xs[N / 16];
-    __shared__ uint4 s_hq[SMAX * F / 16];
-    __shared__ float s_hd[SMAX * NBF];
-    __shared__ int16_t s_hs[SMAX * F / 16];
+    __shared__ float4 s_x[N / 4];                 // core: x_l
+    __shared__ float4 s_wr[NLOG][N / 4];          // core: this workgroup's router rows
+    __shared__ uint4 s_xrec[(XR_WORDS + 3) / 4];  // stream: the Q8_K(x_l) record
+    __shared__ uint4 s_hrec[(HR_WORDS + 3) / 4];  // core: the Q8_K(h) record, all slots
+    __shared__ float s_gsp[NBE];                  // core: shared-gate input partials
+    __shared__ float s_dres[CROWS][SMAX + 1];     // core: per (row, slot) down dots
+    __shared__ float s_xout[CROWS];               // core: x_{l+1} rows to publish
     __shared__ int s_sel[8];
     __shared__ float s_w[8];
-    __shared__ float s_gs;
-    __shared__ float s_red[4];
     __shared__ int s_vote[4][4];
-    __shared__ float4 s_x[N / 4];
-    __shared__ float4 s_wr[4][N / 4];             // router rows of the 4 waves
-    __shared__ float4 s_wsh[N / 4];               // shared-expert gate vector (collector)
 
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
-    const int gw = (int)blockIdx.x * 4 + wv;          // global wave = down row
-    const int nw = (int)gridDim.x * 4;
-    const int half = lane >> 5, l32 = lane & 31;
-    const int gib = l32 >> 2, gg = l32 & 3;            // gate/up task: block, 64-lane group
-    const int ds = lane >> 3, dq = lane & 7;           // down task: slot, task
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), tid = (int)threadIdx.x;
+    const int b = (int)blockIdx.x;
+    const int rep = b % REP;
+    const Rsrc rs = __builtin_amdgcn_make_buffer_rsrc(tg, 0, (int)sizeof(Tagged), 0x00020000);
+    // the 256 logits of replica rep, lane's pairs l and l + 64 (experts
+    // l + 64j, j = 0..3); a half is needed only for an expert below E
+    auto logit_pairs = [&](int E) {
+        return [=](int k) {
+            const int e0 = lane + 128 * k;
+            const int need = (e0 < E ? 1 : 0) | (e0 + 64 < E ? 2 : 0);
+            return need ? 4 * (lane + 64 * k) + need : -1;
+        };
+    };
+    auto read_logits = [&](int E, uint32_t seq, float (&lg)[4]) {
+        uint32_t v[2][2];
+        const bool ok = pollq<2>(rs, TW_LOGITS + rep * 256, logit_pairs(E), seq, v, abort_flag);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            lg[j] = lane + 64 * j < E ? __uint_as_float(v[j >> 1][j & 1]) : -INFINITY;
+        return ok;
+    };
     constexpr size_t GU_ROW = (size_t)NBE * Q4K_BYTES;                 // 1152
     constexpr size_t GU_SLAB = (size_t)F * GU_ROW;                     // 589,824
     constexpr size_t DN_SLAB = (size_t)N * NBF * (TD == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES);
-    const unsigned long long *my_sel = tg->sel[blockIdx.x % REP];
-    const int qk = ((int)blockIdx.x - QWG0) / QWG_STEP;
-    const bool quantiser = wv == 1 && (int)blockIdx.x >= QWG0 && ((int)blockIdx.x - QWG0) % QWG_STEP == 0;
 
-    float xrow = x[gw];            // x_0 of this wave's row (residual input)
-
-    for (int l = 0; l < n_layer; l++) {
-        const qmag_moe_layer &L = layers[l];
-        const int E = L.n_expert, K = L.n_used, S = K + 1;
-        const uint32_t seq = epoch * 256u + (uint32_t)l + 1u;
-        const bool router_wg = (int)blockIdx.x * 4 < max(E, NBE);       // workgroup-uniform
-
-        // optional phase timestamps (100 MHz real-time counter), thread 0 only
+    // optional phase timestamps (100 MHz real-time counter), thread 0 only
 #define TR(i)                                                                              \
     if (trace && threadIdx.x == 0)                                                         \
-        trace[((size_t)blockIdx.x * n_layer + l) * 8 + (i)] = __builtin_amdgcn_s_memrealtime();
-        TR(0);
+        trace[((size_t)b * n_layer + l) * 8 + (i)] = __builtin_amdgcn_s_memrealtime();
 
-        // ---- 1. router workgroups: router rows into LDS, gather x_l, logits;
-        // workgroup 0 also Q8_K(x_l) and, in its wave 0, the collector role
-        bool ok = true;
-        if (router_wg) {
-            if (gw < E) {
-                const float4 *row = (const float4 *)(L.gate_inp + (size_t)gw * N);
+    if (b < CORE) {
+        // ================================================================ core
+        // rows r0 .. r0+15; wave wv owns r0+4wv .. +3, lane i < 4 keeps the
+        // residual value of row r0 + 4wv + i
+        const int r0 = b * CROWS;
+        const int dq = lane & 7, dg = lane >> 3;      // down task: sub-task, lane group
+        // the router rows of layer l go straight into LDS one layer ahead
+        // (layer 0's here, layer l+1's once layer l's logits are computed)
+        auto load_router_rows = [&](const qmag_moe_layer &Ln) {
 #pragma unroll
-                for (int j = 0; j < 8; j++)
-                    __builtin_amdgcn_global_load_lds((const void *)(row + lane + 64 * j),
-                                                     (__attribute__((address_space(3))) void *)&s_wr[wv][64 * j],
-                                                     16, 0, 0);
-            }
-            if (blockIdx.x == 0) {
+            for (int j = 0; j < NLOG; j++) {
+                const int e = NLOG * b + j;
+                if (e < Ln.n_expert) {
+                    const float4 *row = (const float4 *)(Ln.gate_inp + (size_t)e * N);
 #pragma unroll
-                for (int j = 0; j < 2; j++)
-                    __builtin_amdgcn_global_load_lds((const void *)((const float4 *)L.gate_inp_shexp + threadIdx.x + 256 * j),
-                                                     (__attribute__((address_space(3))) void *)&s_wsh[wv * 64 + 256 * j],
-                                                     16, 0, 0);
+                    for (int k = 0; k < 2; k++)
+                        __builtin_amdgcn_global_load_lds((const void *)(row + tid + 256 * k),
+                                                         (__attribute__((address_space(3))) void *)&s_wr[j][64 * wv + 256 * k],
+                                                         16, 0, 0);
+                }
             }
+        };
+        float xres = lane < WROWS ? x[r0 + WROWS * wv + lane] : 0.0f;
+        load_router_rows(layers[0]);
+
+        for (int l = 0; l < n_layer; l++) {
+            const qmag_moe_layer &L = layers[l];
+            const int E = L.n_expert, K = L.n_used, S = K + 1;
+            const uint32_t seq = epoch * 256u + (uint32_t)l + 1u;
+            const bool last = l + 1 == n_layer;
+            TR(0);
+
+            // ---- x_l.  Waves 0-2 poll (wave 3 published this workgroup's
+            // rows last layer; a wave's loads wait for its earlier stores)
+            bool ok = true;
             if (l == 0) {
 #pragma unroll
-                for (int k = 0; k < 2; k++)
-                    s_x[threadIdx.x + 256 * k] = ((const float4 *)x)[threadIdx.x + 256 * k];
-            } else {
-                uint32_t v[8];
-                ok = poll<8>(tg->x, [&](int k) { return 4 * ((int)threadIdx.x + 256 * (k >> 2)) + (k & 3); },
-                             seq, v, abort_flag);
+                for (int k = 0; k < 2; k++) s_x[tid + 256 * k] = ((const float4 *)x)[tid + 256 * k];
+            } else if (wv < 3) {
+                uint32_t v[6][2];
+                auto xp = [&](int k) {
+                    const int p = tid + 192 * k;         // word pair
+                    return p < N / 2 ? 4 * p + 3 : -1;
+                };
+                ok = pollq<6>(rs, TW_X, xp, seq, v, abort_flag);
 #pragma unroll
-                for (int k = 0; k < 2; k++)
-                    s_x[threadIdx.x + 256 * k] =
-                        make_float4(__uint_as_float(v[4 * k]), __uint_as_float(v[4 * k + 1]),
-                                    __uint_as_float(v[4 * k + 2]), __uint_as_float(v[4 * k + 3]));
+                for (int k = 0; k < 6; k++)
+                    if (xp(k) >= 0)
+                        ((float2 *)s_x)[xp(k) >> 2] = make_float2(__uint_as_float(v[k][0]), __uint_as_float(v[k][1]));
             }
-            drain();                 // router rows and gate vector have landed in LDS
-            ok = wg_all(ok, s_vote, 2);
-            if (ok && gw < E) {
-                float s = 0.0f;
+            drain();                 // router rows have landed in LDS
+            if (!wg_all(ok, s_vote, 0)) return;
+            TR(1);
+
+            // ---- logits (waves 0, 1, each published in every replica);
+            // Q8_K(x) block b and its shared-gate partial (wave 2, b < 8)
+            if (wv < NLOG) {
+                const int e = NLOG * b + wv;
+                if (e < E) {
+                    float s = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float4 a = s_x[lane + 64 * j], w = s_wr[wv][lane + 64 * j];
-                    s += w.x * a.x + w.y * a.y + w.z * a.z + w.w * a.w;
+                    for (int j = 0; j < 8; j++) {
+                        const float4 a = s_x[lane + 64 * j], w = s_wr[wv][lane + 64 * j];
+                        s += w.x * a.x + w.y * a.y + w.z * a.z + w.w * a.w;
+                    }
+                    s = group_sum<64>(s);
+                    if (L.router_bias) s += L.router_bias[e];
+                    if (lane < REP) st64(tg->logits[lane] + logit_pos(e), __float_as_uint(s), seq);
+                    if (last && lane == 0) g_logits[e] = s;
                 }
-                s = group_sum<64>(s);
-                if (lane == 0)
-                    st64(tg->logits + gw, __float_as_uint(L.router_bias ? s + L.router_bias[gw] : s), seq);
-            }
-            if (ok && blockIdx.x == 0) {
-                // Q8_K(x_l): wave wv quantises blocks wv and wv+4, publishes them
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const int b = wv + 4 * i;
-                    const Q8Lane q = q8k_quant_lane(s_x[b * 64 + lane]);
-                    ((uint32_t *)s_xq)[b * 64 + lane] = q.packed;
-                    if (lane == 0) s_xd[b] = q.d;
-                    if ((lane & 3) == 0) s_xs[b * 16 + (lane >> 2)] = (int16_t)q.gsum;
-                    unsigned long long *o = tg->xq[l % MAXL];
+            } else if (wv == 2 && b < NBE) {
+                const Q8Lane q = q8k_quant_lane(s_x[b * 64 + lane]);
+                const float4 wsh = ((const float4 *)L.gate_inp_shexp)[b * 64 + lane];
+                const int8_t *q8 = (const int8_t *)&q.packed;
+                float g = wsh.x * (float)q8[0] * q.d + wsh.y * (float)q8[1] * q.d +
+                          wsh.z * (float)q8[2] * q.d + wsh.w * (float)q8[3] * q.d;
+                g = group_sum<64>(g);
+#pragma nounroll
+                for (int r = 0; r < REP; r++) {
+                    unsigned long long *o = tg->xq[r];
                     st64(o + b * 64 + lane, q.packed, seq);
-                    if (lane == 0) st64(o + XQ_D + b, __float_as_uint(q.d), seq);
-                    if ((lane & 3) == 0) st64(o + XQ_S + b * 16 + (lane >> 2), (uint32_t)q.gsum, seq);
+                    if ((lane & 3) == 0) st64(o + XR_S + b * 16 + (lane >> 2), (uint32_t)q.gsum, seq);
+                    if (lane == 0) st64(o + XR_D + b, __float_as_uint(q.d), seq);
+                    if (lane == 1) st64(o + XR_G + b, __float_as_uint(g), seq);
                 }
-                __syncthreads();
-                // shared-expert gate input sum_i wsh[i] * xq[i] * xd[i/256] (nn.c:452-454)
-                {
-                    const int8_t *xq8 = (const int8_t *)s_xq;
-                    float g = 0.0f;
-                    for (int i = (int)threadIdx.x; i < N; i += 256)
-                        g += ((const float *)s_wsh)[i] * (float)xq8[i] * s_xd[i / QK_K];
-                    g = group_sum<64>(g);
-                    if (lane == 0) s_red[wv] = g;
-                }
-                __syncthreads();
-                if (wv == 0) {
-                    // collector: all logits -> top-K -> selection record
-                    uint32_t v[4];
-                    ok = poll<4>(tg->logits, [&](int j) { return lane + 64 * j < E ? lane + 64 * j : -1; },
-                                 seq, v, abort_flag);
-                    float lg[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        lg[j] = lane + 64 * j < E ? __uint_as_float(v[j]) : -INFINITY;
-                        if (lane + 64 * j < E) g_logits[lane + 64 * j] = lg[j];
-                    }
-                    int my_sel = 0;
-                    float my_w = 0.0f;
-                    route_topk(lg, E, K, my_sel, my_w);
-                    const float gs = 1.0f / (1.0f + expf(-((s_red[0] + s_red[1]) + (s_red[2] + s_red[3]))));
-                    // lanes 8..15 take the weights of lanes 0..7
-                    const float w_hi = __shfl(my_w, lane - 8);
-                    if (ok && lane < SEL_WORDS) {
-                        const uint32_t word = lane < 8 ? (uint32_t)my_sel
-                                            : lane < 16 ? __float_as_uint(w_hi) : __float_as_uint(gs);
-                        st64r(tg->sel[0] + lane, word, seq);
-                        if (lane < K) {
-                            g_sel[lane] = my_sel;
-                            g_w[lane] = my_w;
-                        }
-                        if (lane == 16) g_gs[0] = gs;
+            } else if (wv == 3) {
+                // ---- all logits -> softmax, top-K (wave 3 has stored nothing
+                // since last layer's x rows)
+                float lg[4];
+                ok = read_logits(E, seq, lg);
+                int my_sel = 0;
+                float my_w = 0.0f;
+                route_topk(lg, E, K, my_sel, my_w);
+                if (lane < K) {
+                    s_sel[lane] = my_sel;
+                    s_w[lane] = my_w;
+                    if (last && b == 0) {
+                        g_sel[lane] = my_sel;
+                        g_w[lane] = my_w;
                     }
                 }
             }
-        }
-        TR(1);
+            if (!wg_all(ok, s_vote, 1)) return;
+            TR(2);
 
-        // ---- 2. every workgroup: selection record (17 words, wave 0), then
-        // Q8_K(x_l) (648 words, all threads, read once the record is valid)
-        if (wv == 0) {
-            uint32_t v[1];
-            ok = poll<1>(my_sel, [&](int) { return lane < SEL_WORDS && (lane < K || (lane >= 8 && lane < 8 + K) || lane == 16) ? lane : -1; },
-                         seq, v, abort_flag) && ok;
-            if (lane < K) s_sel[lane] = (int)v[0];
-            else if (lane >= 8 && lane < 8 + K) s_w[lane - 8] = __uint_as_float(v[0]);
-            else if (lane == 16) s_gs = __uint_as_float(v[0]);
-        }
-        if (!wg_all(ok, s_vote, 0)) return;
-        TR(2);
-
-        // ---- 3. this wave's gate/up and down bytes (routed slots and the
-        // shared slot), all issued before any is consumed
-        uint4 gh[MAX_RP], g0[MAX_RP], g1[MAX_RP];
+            // ---- this wave's down rows of every slot into registers, and
+            // the next layer's router rows (this layer's are consumed)
+            DRaw<TD> dr[DN_ROUNDS];
 #pragma unroll
-        for (int j = 0; j < MAX_RP; j++) {
-            gh[j] = g0[j] = g1[j] = make_uint4(0, 0, 0, 0);
-            const int rp = gw + j * nw;
-            const int slot = rp / F;
-            if (rp < S * F) {
-                const uint8_t *m = slot < K ? (const uint8_t *)(half ? L.up_exps : L.gate_exps) +
-                                                  (size_t)s_sel[slot] * GU_SLAB
-                                            : (const uint8_t *)(half ? L.up_shexp : L.gate_shexp);
-                const uint8_t *blk = m + (size_t)(rp % F) * GU_ROW + (size_t)gib * Q4K_BYTES;
-                gh[j] = ld16(blk);
-                g0[j] = ld16(blk + 16 + 32 * gg);
-                g1[j] = ld16(blk + 32 + 32 * gg);
+            for (int j = 0; j < DN_ROUNDS; j++) {
+                d_zero(dr[j]);
+                const int t = 8 * j + dg;                // (row, slot) pair: row t & 3, slot t >> 2
+                if (t < WROWS * S) {
+                    const int slot = t >> 2, row = r0 + WROWS * wv + (t & 3);
+                    const uint8_t *slab = slot < K ? (const uint8_t *)L.down_exps + (size_t)s_sel[slot] * DN_SLAB
+                                                   : (const uint8_t *)L.down_shexp;
+                    d_load<TD>(dr[j], slab, row, dq);
+                }
             }
-        }
-        DRaw<TD> dsh, drt;
-        d_zero(dsh);
-        d_zero(drt);
-        if (ds < K) d_load<TD>(drt, (const uint8_t *)L.down_exps + (size_t)s_sel[ds] * DN_SLAB, gw, dq);
-        if (lane < 8) d_load<TD>(dsh, (const uint8_t *)L.down_shexp, gw, dq);
-        if (blockIdx.x != 0) {      // workgroup 0 quantised x itself
-            uint32_t v[3];
-            auto xi = [&](int k) {
-                const int i = (int)threadIdx.x + 256 * k;
-                return i < XQ_WORDS ? i : -1;
-            };
-            // written by workgroup 0 before its selection record: read cached
-            ok = read_bulk<3>(tg->xq[l % MAXL], xi, seq, v, abort_flag);
-#pragma unroll
-            for (int k = 0; k < 3; k++) {
-                const int i = xi(k);
-                if (i < 0) continue;
-                if (i < XQ_D) ((uint32_t *)s_xq)[i] = v[k];
-                else if (i < XQ_S) s_xd[i - XQ_D] = __uint_as_float(v[k]);
-                else s_xs[i - XQ_S] = (int16_t)(int)v[k];
-            }
-        }
-        if (!wg_all(ok, s_vote, 1)) return;
-        TR(3);
+            if (!last) load_router_rows(layers[l + 1]);
+            TR(3);
 
-        // ---- 4. gate/up rows -> h = silu(g) * u, published for the quantisers
-        {
+            // ---- wave 0: the 2S block sentinels and the 8 shared-gate partials
+            if (wv == 0) {
+                uint32_t v[1];
+                const unsigned long long *src = lane < 32 ? tg->hq : tg->xq[rep];
+                ok = poll<1>(src, [&](int) {
+                    return lane < 2 * S ? HR_D + lane : (lane >= 32 && lane < 32 + NBE) ? XR_G + lane - 32 : -1;
+                }, seq, v, abort_flag);
+                if (lane >= 32 && lane < 32 + NBE) s_gsp[lane - 32] = __uint_as_float(v[0]);
+            }
+            if (!wg_all(ok, s_vote, 2)) return;
+            {
+                // word pairs; the used ranges start and end on even words
+                uint32_t v[HQ_PAIRS_PER_THREAD][2];
+                auto hp = [&](int k) {
+                    const int p = tid + 256 * k, i = 2 * p;
+                    const bool used = i < HR_D ? i < 2 * S * 64 : i < HR_S ? i < HR_D + 2 * S : i < HR_S + 2 * S * 16;
+                    return used ? 4 * p + 3 : -1;
+                };
+                ok = pollq<HQ_PAIRS_PER_THREAD>(rs, TW_HQ, hp, seq, v, abort_flag);
+#pragma unroll
+                for (int k = 0; k < HQ_PAIRS_PER_THREAD; k++)
+                    if (hp(k) >= 0) ((uint2 *)s_hrec)[hp(k) >> 2] = make_uint2(v[k][0], v[k][1]);
+            }
+            if (!wg_all(ok, s_vote, 3)) return;
+            TR(5);
+
+            // ---- down dots, then combine in the reference order (nn.c:614-629)
+#pragma unroll
+            for (int j = 0; j < DN_ROUNDS; j++) {
+                const int t = 8 * j + dg;
+                if (8 * j < WROWS * S) {                 // wave-uniform
+                    const int slot = t < WROWS * S ? t >> 2 : 0;
+                    float v = d_dot<TD>(dr[j], (const uint32_t *)s_hrec + slot * (F / 4),
+                                        (const float *)s_hrec + HR_D + slot * NBF,
+                                        (const int *)s_hrec + HR_S + slot * (F / 16), dq);
+                    v = group_sum<8>(v);
+                    if (dq == 0 && t < WROWS * S) s_dres[WROWS * wv + (t & 3)][slot] = v;
+                }
+            }
+            __syncthreads();
+            if (lane < WROWS) {
+                float g = 0.0f;
+#pragma unroll
+                for (int k = 0; k < NBE; k++) g += s_gsp[k];
+                const float gs = 1.0f / (1.0f + expf(-g));
+                if (last && b == 0 && wv == 0 && lane == 0) g_gs[0] = gs;
+                const float *dres = s_dres[WROWS * wv + lane];
+                float acc = 0.0f;
+                for (int k = 0; k < K; k++) acc = __fadd_rn(acc, __fmul_rn(s_w[k], dres[k]));
+                acc = __fadd_rn(acc, __fmul_rn(gs, dres[K]));
+                if (out) {
+                    out[r0 + WROWS * wv + lane] = acc;
+                } else {
+                    xres = __fadd_rn(acc, xres);
+                    s_xout[WROWS * wv + lane] = xres;
+                }
+            }
+            __syncthreads();
+            // wave 3 publishes the workgroup's 16 rows with one store
+            if (!out && wv == 3 && lane < CROWS) {
+                if (!last) st64(tg->x + r0 + lane, __float_as_uint(s_xout[lane]), seq + 1u);
+                else x[r0 + lane] = s_xout[lane];
+            }
+            TR(6);
+        }
+    } else {
+        // ============================================================== stream
+        const int gwv = (b - CORE) * 4 + wv;
+        const int half = lane >> 5, l32 = lane & 31;
+        const int gib = l32 >> 2, gg = l32 & 3;       // gate/up task: block, 64-lane group
+        // wave 1 of workgroup QWG0 + k*QWG_STEP quantises h block k
+        const int qk = (b - QWG0) / QWG_STEP;
+        const bool quantiser = wv == 1 && b >= QWG0 && (b - QWG0) % QWG_STEP == 0;
+
+        for (int l = 0; l < n_layer; l++) {
+            const qmag_moe_layer &L = layers[l];
+            const int E = L.n_expert, K = L.n_used, S = K + 1;
+            const uint32_t seq = epoch * 256u + (uint32_t)l + 1u;
+            const bool last = l + 1 == n_layer;
+            TR(0);
+
+            // ---- all logits -> softmax, top-K (wave 0).  These workgroups
+            // wait here through the core's part of the layer: one word first.
+            bool ok = true;
+            if (wv == 0) {
+                uint32_t g1[1];
+                ok = poll<1>(tg->logits[rep], [&](int) { return lane == 0 ? logit_pos((b * 37) % E) : -1; }, seq, g1,
+                             abort_flag);
+                float lg[4];
+                ok = ok && read_logits(E, seq, lg);
+                TR(7);
+                int my_sel = 0;
+                float my_w = 0.0f;
+                route_topk(lg, E, K, my_sel, my_w);
+                if (lane < K) s_sel[lane] = my_sel;
+                TR(6);
+            }
+            if (!wg_all(ok, s_vote, 1)) return;
+            TR(2);
+
+            // ---- gate/up row pairs of this wave, then Q8_K(x_l)
+            uint4 gh[MAX_RP], g0[MAX_RP], g1[MAX_RP];
+#pragma unroll
+            for (int j = 0; j < MAX_RP; j++) {
+                gh[j] = g0[j] = g1[j] = make_uint4(0, 0, 0, 0);
+                const int rp = gwv + j * GU_WAVES;
+                const int slot = rp / F;
+                if (rp < S * F) {
+                    const uint8_t *m = slot < K ? (const uint8_t *)(half ? L.up_exps : L.gate_exps) +
+                                                      (size_t)s_sel[slot] * GU_SLAB
+                                                : (const uint8_t *)(half ? L.up_shexp : L.gate_shexp);
+                    const uint8_t *blk = m + (size_t)(rp % F) * GU_ROW + (size_t)gib * Q4K_BYTES;
+                    gh[j] = ld16(blk);
+                    g0[j] = ld16(blk + 16 + 32 * gg);
+                    g1[j] = ld16(blk + 32 + 32 * gg);
+                }
+            }
+            {
+                uint32_t v[2][2];
+                auto xp = [&](int k) {
+                    const int p = tid + 256 * k;       // word pair (the whole record is written)
+                    return p < XR_WORDS / 2 ? 4 * p + 3 : -1;
+                };
+                ok = pollq<2>(rs, TW_XQ + rep * XR_WORDS, xp, seq, v, abort_flag);
+#pragma unroll
+                for (int k = 0; k < 2; k++)
+                    if (xp(k) >= 0) ((uint2 *)s_xrec)[xp(k) >> 2] = make_uint2(v[k][0], v[k][1]);
+            }
+            if (!wg_all(ok, s_vote, 2)) return;
+            TR(3);
+
+            // ---- h = silu(g) * u for the wave's row pairs, one store for all
             Q4Act a;
-            const uint4 *xw = s_xq + (gib * QK_K + 64 * gg) / 16;
+            const uint4 *xw = s_xrec + (gib * QK_K + 64 * gg) / 16;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const uint4 w = xw[k];
@@ -488,98 +620,46 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 a.x[4 * k + 2] = w.z;
                 a.x[4 * k + 3] = w.w;
             }
-            a.xd = s_xd[gib];
-            const int16_t *sp = s_xs + gib * 16 + 4 * gg;
+            a.xd = ((const float *)s_xrec)[XR_D + gib];
+            const int *sp = (const int *)s_xrec + XR_S + gib * 16 + 4 * gg;
             a.sx0 = (float)(sp[0] + sp[1]);
             a.sx1 = (float)(sp[2] + sp[3]);
+            float my_h = 0.0f;
 #pragma unroll
             for (int j = 0; j < MAX_RP; j++) {
-                const int rp = gw + j * nw;
-                if (rp < S * F) {                       // wave-uniform
+                if (gwv + j * GU_WAVES < S * F) {          // wave-uniform
                     float v = q4_task(gh[j], g0[j], g1[j], a, gg);
                     v = group_sum<32>(v);
                     auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
                                                                false, false);
                     const float u = __uint_as_float(pr[1]);
-                    if (lane == 0) st64(tg->h + rp, __float_as_uint((v / (1.0f + expf(-v))) * u), seq);
+                    const float hv = (v / (1.0f + expf(-v))) * u;
+                    if (lane == j) my_h = hv;
                 }
             }
-        }
-        TR(4);
+            if (lane < MAX_RP && gwv + lane * GU_WAVES < S * F)
+                st64(tg->h + gwv + lane * GU_WAVES, __float_as_uint(my_h), seq);
+            TR(4);
 
-        // ---- 5. quantiser waves publish Q8_K(h) blocks; every workgroup
-        // polls the 18 block sentinels, then reads the blocks into LDS
-        ok = true;
-        if (quantiser && qk < S * NBF) {
-            uint32_t v[4];
-            ok = poll<4>(tg->h, [&](int k) { return qk * QK_K + 4 * lane + k; }, seq, v, abort_flag);
-            const float4 hv = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]),
-                                          __uint_as_float(v[2]), __uint_as_float(v[3]));
-            *(float4 *)(g_h + qk * QK_K + 4 * lane) = hv;              // stage copy
-            const Q8Lane q = q8k_quant_lane(hv);
-            unsigned long long *o = tg->hq[l % MAXL] + qk * HQ_BLK;
-            st64(o + lane, q.packed, seq);
-            if ((lane & 3) == 0) st64(o + 65 + (lane >> 2), (uint32_t)q.gsum, seq);
-            if (lane == 0) st64(o + 64, __float_as_uint(q.d), seq);  // sentinel, written last
-        }
-        if (wv == 0) {
-            uint32_t v[1];
-            ok = poll<1>(tg->hq[l % MAXL], [&](int) { return lane < S * NBF ? lane * HQ_BLK + 64 : -1; }, seq, v,
-                         abort_flag) && ok;
-        }
-        if (!wg_all(ok, s_vote, 2)) return;
-        {
-            uint32_t v[HQ_PER_THREAD];
-            auto hi = [&](int k) {
-                const int i = (int)threadIdx.x + 256 * k;
-                return i < S * NBF * HQ_BLK ? i : -1;
-            };
-            ok = read_bulk<HQ_PER_THREAD>(tg->hq[l % MAXL], hi, seq, v, abort_flag);
-#pragma unroll
-            for (int k = 0; k < HQ_PER_THREAD; k++) {
-                const int i = hi(k);
-                if (i < 0) continue;
-                const int b = i / HQ_BLK, r = i % HQ_BLK;
-                if (r < 64) ((uint32_t *)s_hq)[b * 64 + r] = v[k];
-                else if (r == 64) s_hd[b] = __uint_as_float(v[k]);
-                else s_hs[b * 16 + r - 65] = (int16_t)(int)v[k];
+            // ---- quantiser: h block qk -> Q8_K(h) block record
+            if (quantiser && qk < S * NBF) {
+                uint32_t v[2][2];
+                ok = pollq<2>(rs, TW_H, [&](int k) { return 4 * (qk * (QK_K / 2) + 2 * lane + k) + 3; }, seq, v,
+                              abort_flag);
+                const float4 hv = make_float4(__uint_as_float(v[0][0]), __uint_as_float(v[0][1]),
+                                              __uint_as_float(v[1][0]), __uint_as_float(v[1][1]));
+                if (last) *(float4 *)(g_h + qk * QK_K + 4 * lane) = hv;      // stage copy
+                const Q8Lane q = q8k_quant_lane(hv);
+                unsigned long long *o = tg->hq;
+                st64(o + qk * 64 + lane, q.packed, seq);
+                if ((lane & 3) == 0) st64(o + HR_S + qk * 16 + (lane >> 2), (uint32_t)q.gsum, seq);
+                if (lane == 0) st64(o + HR_D + qk, __float_as_uint(q.d), seq);
             }
+            // LDS is rewritten next layer only after this barrier
+            __syncthreads();
         }
-        if (!wg_all(ok, s_vote, 3)) return;
-        TR(5);
-
-        // ---- 6. down row gw of the routed experts (8 lanes each) and of the
-        // shared expert (lanes 0-7), combined in the reference order
-        {
-            const int slot = ds < K ? ds : 0;
-            float dr = d_dot<TD>(drt, (const uint32_t *)s_hq + slot * (F / 4), s_hd + slot * NBF,
-                                 s_hs + slot * (F / 16), dq);
-            dr = group_sum<8>(dr);
-            float dsv = d_dot<TD>(dsh, (const uint32_t *)s_hq + K * (F / 4), s_hd + K * NBF,
-                                  s_hs + K * (F / 16), dq);
-            dsv = group_sum<8>(dsv);
-            float acc = 0.0f;
-            for (int k = 0; k < K; k++) {
-                const float dk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dr), 8 * k));
-                acc = __fadd_rn(acc, __fmul_rn(s_w[k], dk));
-            }
-            const float dsh0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsv), 0));
-            acc = __fadd_rn(acc, __fmul_rn(s_gs, dsh0));
-            if (out) {
-                if (lane == 0) out[gw] = acc;
-            } else {
-                xrow = __fadd_rn(acc, xrow);
-                if (lane == 0) {
-                    if (l + 1 < n_layer) st64(tg->x + gw, __float_as_uint(xrow), seq + 1u);
-                    else x[gw] = xrow;
-                }
-            }
-        }
-        TR(6);
-#undef TR
-        // LDS is rewritten next layer only after this barrier
-        __syncthreads();
     }
+#undef TR
 }
 
 }  // namespace fused

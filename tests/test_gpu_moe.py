@@ -125,20 +125,39 @@ def test_moe_layer_fused_small_routing(qm, orc, n_used, n_expert):
 
 
 def test_moe_decode_paths_agree_40_layers(qm, orc):
-    """40 layers x 3 tokens: fused kernel vs launch sequence (independent
-    kernels), same resident weights."""
+    """40 qwen35moe layers x 2 tokens.
+
+    1. Teacher-forced, layer by layer: on the persistent kernel's own x_l,
+       one layer through the persistent kernel and through the launch
+       sequence (independent kernels) agree to 1e-4 of max|y|.
+    2. One 40-layer launch of the persistent kernel equals the same kernel
+       applied one layer per launch bit for bit, so the hand-off of x between
+       layers inside the kernel adds nothing.
+    End to end the two paths are not compared at 1e-4: their fp32 sums are
+    associated differently (router dot, softmax sum, shared gate), which
+    moves h in the last bit and, rarely, one Q8_K(h) value by one step; over
+    40 residual layers these steps reach ~1e-4 by themselves."""
     rls = [qm.ResidentLayer(seed=404, layer=l) for l in range(40)]
-    x = orc.fill_normal(41, 3 * 2048, 0.0, 1.0)
-    outs = []
-    for fused in (True, False):
-        qm.set_fused(fused)
-        xb = qm.DBuf.from_array(x)
-        qm.moe_stack_dev([r.c for r in rls], xb.ptr, 3)
-        qm.sync()
-        outs.append(xb.download(np.float32).reshape(3, 2048))
-    qm.set_fused(True)
-    for t in range(3):
-        assert max_rel_err(outs[0][t], outs[1][t]) < TOL
+    cl = [r.c for r in rls]
+    x = orc.fill_normal(41, 2 * 2048, 0.0, 1.0)
+    for t in range(2):
+        xt = x[t * 2048:(t + 1) * 2048]
+        # 1. layer-by-layer teacher forcing
+        xl = xt.copy()
+        for l in range(40):
+            outs = []
+            for fused in (True, False):
+                qm.set_fused(fused)
+                outs.append(run_layer(qm, rls[l], xl, 1)[0])
+            qm.set_fused(True)
+            assert max_rel_err(outs[0], outs[1]) < TOL, f"token {t} layer {l}"
+            xb = qm.DBuf.from_array(xl)
+            qm.moe_stack_dev([cl[l]], xb.ptr, 1)          # x_{l+1} = x_l + moe_l(x_l)
+            xl = xb.download(np.float32)
+        # 2. one launch over all 40 layers
+        xb = qm.DBuf.from_array(xt)
+        qm.moe_stack_dev(cl, xb.ptr, 1)
+        assert np.array_equal(xb.download(np.float32).view(np.uint32), xl.view(np.uint32))
     for r in rls:
         r.close()
 
