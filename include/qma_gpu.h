@@ -89,7 +89,8 @@ int qmag_event_elapsed(int a, int b, float *ms);
    enabled, every kernel the MoE entries launch is bracketed by HIP events on
    the library stream.  Kernel ids: 0 router, 1 top-k/Q8_K(x), 2 gate/up,
    3 Q8_K(h), 4 down+combine, 5 fused decode, 6 matvec (matmul entries),
-   7 Q8_K quantisation (every launch of it).  qmag_prof_read synchronises and
+   7 Q8_K quantisation (every launch of it), 8 grouping (prefill), 9 combine
+   (prefill).  qmag_prof_read synchronises and
    returns the launch count and summed milliseconds of one id. */
 int qmag_prof_enable(int on);
 int qmag_prof_read(int kernel_id, long *count, double *total_ms);
@@ -114,6 +115,12 @@ int qmag_prof_read(int kernel_id, long *count, double *total_ms);
    QMAG_ERR_KERNEL by qmag_sync, never a hang).  The ordinary launch is the
    default: equally fast, and visible to rocprofv3's kernel tracing. */
 #define QMAG_OPT_COOP 3
+/* QMAG_OPT_GROUPED (default 1): qmag_moe_ffn_dev with T >= 8 tokens (the
+   prefill form) runs the grouped expert GEMM: (token, slot) pairs bucketed
+   by expert, gate/up and down as int8 MFMA tiles of 16 pairs, each expert's
+   weights read once per 16 pairs; 0 selects the per-token launch sequence
+   (same results within the fp32 tolerance). */
+#define QMAG_OPT_GROUPED 4
 int qmag_set_option(int option, int value);
 int qmag_trace_read(void *dst, size_t bytes);
 
@@ -163,10 +170,12 @@ int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *out, int T)
    qma_eval, nn.c:2252).  x: f32 [n_tok][n_embd], updated in place. */
 int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, float *x, int n_tok);
 
-/* Stage outputs of the last qmag_moe_ffn_dev / qmag_moe_stack_dev layer for
-   token 0 (device pointers the library owns, valid until the next call):
+/* Stage outputs of the last qmag_moe_ffn_dev / qmag_moe_stack_dev layer
+   (device pointers the library owns, valid until the next call):
    logits f32[n_expert], sel i32[n_used], w f32[n_used], gs f32[1],
-   h f32[(n_used+1)][n_ff] (slot n_used = shared expert). */
+   h f32[(n_used+1)][n_ff] (slot n_used = shared expert) for token 0; after
+   a qmag_moe_ffn_dev call on T > 1 tokens each array holds all T tokens,
+   token-major ([T][n_expert], [T][n_used], ..., [T][n_used+1][n_ff]). */
 int qmag_moe_last_stage(const float **logits, const int **sel, const float **w,
                         const float **gs, const float **h);
 

@@ -41,6 +41,8 @@ enum WsSlot {
     WS_LAYERS,                      // device copy of layer descriptors
     WS_OUT,                         // layer output scratch
     WS_FLAGS,                       // kernel status / counters
+    WS_GRP,                         // grouped prefill: bucket counts/offsets, pair permutation
+    WS_Y,                           // grouped prefill: per-pair down outputs
     WS_COUNT
 };
 void *workspace(int slot, size_t bytes, int *status);
@@ -48,6 +50,7 @@ void *workspace(int slot, size_t bytes, int *status);
 // ---- per-kernel event timing (qmag_prof_*) ----
 enum ProfId {
     PROF_ROUTER = 0, PROF_TOPK, PROF_GATEUP, PROF_HQUANT, PROF_DOWN, PROF_FUSED, PROF_MATVEC, PROF_Q8K,
+    PROF_GROUP, PROF_COMBINE,
     PROF_COUNT
 };
 bool prof_on();
@@ -62,6 +65,12 @@ int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const 
 int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const float *resid,
             hipStream_t s);
 int moe_check_layer(const qmag_moe_layer *L);
+
+// grouped prefill (qmag_prefill.hip)
+int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *logits, hipStream_t s);
+int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, const float *gs,
+                const int8_t *xq, const float *xd, const int16_t *xs, float *h, int8_t *hq, float *hd,
+                int16_t *hs, const float *resid, float *out, hipStream_t s);
 
 // persistent single-launch decode (qmag_fused.hip)
 bool fused_eligible(const qmag_moe_layer *L, int n_layer);

@@ -294,6 +294,11 @@ __global__ __launch_bounds__(256) void down_kernel(const uint8_t *__restrict__ d
 // ------------------------------------------------------------------ host --
 static bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
 
+// batches of at least this many tokens take the grouped expert GEMM
+// (qmag_prefill.hip) when QMAG_OPT_GROUPED is on; smaller ones the
+// per-token launch sequence below
+constexpr int GROUPED_MIN_T = 8;
+
 int moe_check_layer(const qmag_moe_layer *L)
 {
     if (!L) return fail(QMAG_ERR_ARG, "moe: null layer");
@@ -398,15 +403,28 @@ int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const fl
     st = moe_ws(L, T, ws);
     if (st) return st;
     const int N = L->n_embd, F = L->n_ff, E = L->n_expert, K = L->n_used, S = K + 1;
+    const bool grouped = T >= GROUPED_MIN_T && option(QMAG_OPT_GROUPED);
 
     prof_begin(PROF_ROUTER, s);
-    hipLaunchKernelGGL(router_kernel, dim3((E * T + 3) / 4), dim3(256), 0, s, L->gate_inp,
-                       L->router_bias, x, N, E, T, ws.logits);
+    if (grouped) {
+        st = launch_router_mfma(L, x, T, ws.logits, s);
+        if (st) return st;
+    } else {
+        hipLaunchKernelGGL(router_kernel, dim3((E * T + 3) / 4), dim3(256), 0, s, L->gate_inp,
+                           L->router_bias, x, N, E, T, ws.logits);
+    }
     prof_end(PROF_ROUTER, s);
     prof_begin(PROF_TOPK, s);
     hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(256), 0, s, ws.logits, x, L->gate_inp_shexp, N,
                        E, K, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs);
     prof_end(PROF_TOPK, s);
+    if (grouped) {
+        st = moe_grouped(L, T, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs, ws.h, ws.hq, ws.hd, ws.hs, resid, out, s);
+        if (st) return st;
+        g_last = ws;
+        g_last_K = K;
+        return QMAG_OK;
+    }
     for (int t = 0; t < T; t++) {
         prof_begin(PROF_GATEUP, s);
         switch (N / QK_K) {

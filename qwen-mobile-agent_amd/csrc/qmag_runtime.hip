@@ -23,11 +23,13 @@ Ctx &ctx() { return g_ctx; }
 static int g_opt_fused = 1;
 static int g_opt_trace = 0;
 static int g_opt_coop = 0;
+static int g_opt_grouped = 1;
 int option(int id)
 {
     if (id == QMAG_OPT_FUSED) return g_opt_fused;
     if (id == QMAG_OPT_TRACE) return g_opt_trace;
     if (id == QMAG_OPT_COOP) return g_opt_coop;
+    if (id == QMAG_OPT_GROUPED) return g_opt_grouped;
     return 0;
 }
 
@@ -278,6 +280,10 @@ int qmag_set_option(int opt, int value)
     }
     if (opt == QMAG_OPT_COOP) {
         g_opt_coop = value != 0;
+        return QMAG_OK;
+    }
+    if (opt == QMAG_OPT_GROUPED) {
+        g_opt_grouped = value != 0;
         return QMAG_OK;
     }
     return fail(QMAG_ERR_ARG, "unknown option %d", opt);

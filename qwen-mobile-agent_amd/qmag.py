@@ -123,6 +123,15 @@ def set_coop(on: bool) -> None:
     check(lib().qmag_set_option(OPT_COOP, 1 if on else 0))
 
 
+OPT_GROUPED = 4
+
+
+def set_grouped(on: bool) -> None:
+    """Batches of >= 8 tokens: the grouped int8-MFMA expert GEMM (default) or
+    the per-token launch sequence."""
+    check(lib().qmag_set_option(OPT_GROUPED, 1 if on else 0))
+
+
 def trace_read(n_layer: int) -> np.ndarray:
     """Phase timestamps of the last fused launch: uint64 [512][n_layer][8],
     device real-time counter at 100 MHz."""
@@ -218,14 +227,20 @@ def moe_stack_dev(layers, x_ptr: int, n_tok: int) -> None:
     check(lib().qmag_moe_stack_dev(arr, len(layers), x_ptr, n_tok))
 
 
-def moe_last_stage(n_expert: int, n_used: int, n_ff: int):
+def moe_last_stage(n_expert: int, n_used: int, n_ff: int, n_tok: int = 0):
+    """Stage outputs of the last MoE call for token 0 (n_tok = 0), or, after
+    a multi-token qmag_moe_ffn_dev call, for its first n_tok tokens (arrays
+    gain a leading token axis)."""
     ptrs = [P() for _ in range(5)]
     check(lib().qmag_moe_last_stage(*[C.byref(p) for p in ptrs]))
-    logits = d2h_ptr(ptrs[0].value, np.float32, n_expert)
-    sel = d2h_ptr(ptrs[1].value, np.int32, n_used)
-    w = d2h_ptr(ptrs[2].value, np.float32, n_used)
-    gs = d2h_ptr(ptrs[3].value, np.float32, 1)[0]
-    h = d2h_ptr(ptrs[4].value, np.float32, (n_used + 1) * n_ff).reshape(n_used + 1, n_ff)
+    T = max(n_tok, 1)
+    logits = d2h_ptr(ptrs[0].value, np.float32, T * n_expert).reshape(T, n_expert)
+    sel = d2h_ptr(ptrs[1].value, np.int32, T * n_used).reshape(T, n_used)
+    w = d2h_ptr(ptrs[2].value, np.float32, T * n_used).reshape(T, n_used)
+    gs = d2h_ptr(ptrs[3].value, np.float32, T)
+    h = d2h_ptr(ptrs[4].value, np.float32, T * (n_used + 1) * n_ff).reshape(T, n_used + 1, n_ff)
+    if n_tok == 0:
+        return dict(logits=logits[0], sel=sel[0], w=w[0], gs=gs[0], h=h[0])
     return dict(logits=logits, sel=sel, w=w, gs=gs, h=h)
 
 
@@ -242,7 +257,7 @@ def quantize_dev(x_ptr: int, n: int, wtype: int, out_ptr: int) -> None:
 
 
 PROF_IDS = {"router": 0, "topk": 1, "gateup": 2, "hquant": 3, "down": 4, "fused": 5, "matvec": 6,
-            "q8k": 7}
+            "q8k": 7, "group": 8, "combine": 9}
 
 
 def prof_enable(on: bool) -> None:

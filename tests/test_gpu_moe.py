@@ -167,7 +167,103 @@ def test_moe_layer_prefill_skewed_router(qm, orc):
     rl = qm.ResidentLayer(seed=9, layer=0, router_bias_std=1.0)
     hl = host_of(orc, rl)
     x = orc.fill_normal(15, 16 * 2048, 0.0, 1.0)
-    check_layer(qm, orc, rl, hl, x, 16)
+    check_layer_staged(qm, orc, rl, hl, x, 16)
+    rl.close()
+
+
+def check_layer_staged(qm, orc, rl, hl, x, T, stage1_tokens=None):
+    """All T tokens, stage by stage with teacher forcing (for batches, where
+    many tokens are compared):
+      1. logits, selection (outside near-ties), weights and shared gate
+         against the oracle's router on the same x;
+      2. h per (token, slot) against the oracle's gate/up + SwiGLU of the
+         expert the GPU selected;
+      3. the output against the oracle's down projection (Q8_K of the GPU's
+         own h, requantised on the host) and combine, with the GPU's weights.
+    Stage 3 starts from the GPU's h so that a last-bit difference in h --
+    the fp32 epilogues are associated differently -- which moves one Q8_K(h)
+    value by one step cannot fake or mask an error in the down projection;
+    stage 2 bounds that difference at the 1e-4 tolerance."""
+    N, F, E, K = hl.n_embd, hl.n_ff, hl.n_expert, hl.n_used
+    S = K + 1
+    got = run_layer(qm, rl, x, T)
+    st = qm.moe_last_stage(E, K, F, n_tok=T)
+    gb, db = hl.gate_exps.size // E, hl.down_exps.size // E
+    tokens = range(T) if stage1_tokens is None else stage1_tokens
+    for t in tokens:
+        xt = x[t * N:(t + 1) * N]
+        sel_o, w_o, lg_o = orc.moe_route(hl, xt)
+        assert max_rel_err(st["logits"][t], lg_o) < TOL, f"logits, token {t}"
+        if route_margin(lg_o, K) > TIE:
+            assert list(st["sel"][t]) == list(sel_o), f"selection, token {t}"
+            assert np.allclose(st["w"][t], w_o, rtol=1e-5, atol=1e-7), f"weights, token {t}"
+        xq, xd, xs = orc.q8k_quant(xt)
+        assert abs(st["gs"][t] - orc.moe_shared_gate(hl.gate_inp_shexp, xq, xd, N)) < 1e-6
+        for s in range(S):
+            if s < K:
+                e = int(st["sel"][t][s])
+                ge, ue = hl.gate_exps[e * gb:(e + 1) * gb], hl.up_exps[e * gb:(e + 1) * gb]
+            else:
+                ge, ue = hl.gate_shexp, hl.up_shexp
+            h = orc.moe_expert_h(ge, ue, N, F, xq, xd, xs)
+            assert max_rel_err(st["h"][t][s], h) < TOL, f"h, token {t} slot {s}"
+    for t in range(T):
+        acc = np.zeros(N, np.float32)
+        for s in range(S):
+            if s < K:
+                e = int(st["sel"][t][s])
+                dn, wt, scale = hl.down_exps[e * db:(e + 1) * db], hl.t_down_exps, st["w"][t][s]
+            else:
+                dn, wt, scale = hl.down_shexp, hl.t_down_shexp, st["gs"][t]
+            y = orc.matmul_q8k(st["h"][t][s], dn, F, N, 1, wt)[0]
+            acc = (acc + (np.float32(scale) * y).astype(np.float32)).astype(np.float32)
+        assert max_rel_err(got[t], acc) < TOL, f"output, token {t}"
+    return got
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(n_embd=512, n_ff=256, n_expert=16, n_used=4, t_down=14),
+    dict(n_embd=256, n_ff=512, n_expert=12, n_used=8, t_down=12),
+    dict(n_embd=1024, n_ff=1024, n_expert=64, n_used=6, t_down=14),
+    dict(n_embd=2048, n_ff=512, n_expert=32, n_used=8, t_down=12),
+])
+def test_moe_grouped_small_shapes(qm, orc, cfg):
+    """Batches of >= 8 tokens run the grouped int8-MFMA expert GEMM; ragged
+    counts (37 tokens) leave partial 16-pair blocks in most buckets."""
+    hl = make_host_layer(orc, seed=13, **cfg)
+    rl = qm.ResidentLayer.from_host(hl)
+    for T in (8, 37):
+        x = orc.fill_normal(300 + T, T * cfg["n_embd"], 0.0, 1.0)
+        check_layer_staged(qm, orc, rl, hl, x, T)
+    rl.close()
+
+
+def test_moe_grouped_sequence_option(qm, orc):
+    """QMAG_OPT_GROUPED = 0 sends a batch through the per-token launch
+    sequence, which is checked against the oracle the same way."""
+    hl = make_host_layer(orc, seed=17, n_embd=512, n_ff=256, n_expert=16, n_used=4, t_down=14)
+    rl = qm.ResidentLayer.from_host(hl)
+    x = orc.fill_normal(77, 12 * 512, 0.0, 1.0)
+    qm.set_grouped(False)
+    try:
+        check_layer_staged(qm, orc, rl, hl, x, 12)
+    finally:
+        qm.set_grouped(True)
+    rl.close()
+
+
+def test_moe_prefill_c5_shape(qm, orc):
+    """C5: 512 tokens, router skewed by a per-expert bias ~N(0,1) (4096
+    routed pairs over a skewed set of experts), against the oracle: every
+    token's output (stage 3), the router and h of every 8th token."""
+    rl = qm.ResidentLayer(seed=55, layer=0, router_bias_std=1.0)
+    hl = host_of(orc, rl)
+    x = orc.fill_normal(512, 512 * 2048, 0.0, 1.0)
+    orc.set_threads(8)
+    try:
+        check_layer_staged(qm, orc, rl, hl, x, 512, stage1_tokens=range(0, 512, 8))
+    finally:
+        orc.set_threads(1)
     rl.close()
 
 
