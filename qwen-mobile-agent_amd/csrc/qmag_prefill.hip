@@ -7,8 +7,10 @@
 //                        expert is bucket E with one pair per token
 //   gateup_grouped_kernel h = silu(x.G) * (x.U) per pair: 16 pairs x 16 rows
 //                        per wave, one v_mfma_i32_16x16x32_i8 per 32-wide
-//                        Q4_K sub-block, the sub-block scale and min applied
-//                        to the int32 results
+//                        Q4_K sub-block with its 6-bit scale applied to the
+//                        int32 result, and one more against the sub-block's
+//                        min broadcast over its 32 k (the min term, summed in
+//                        the matrix core over the super-block)
 //   q8k_quant_kernel     Q8_K(h) per pair
 //   down_grouped_kernel  y[pair] = Q8_K(h) . D^T: Q6_K per 16-wide group (the
 //                        MFMA's other 16 k are zero) or Q4_K per sub-block
@@ -53,33 +55,46 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
     const float4 *xr = (const float4 *)(x + (size_t)(tok < T ? tok : 0) * N + q * seg);
     const float4 *wr = (const float4 *)(Wr + (size_t)(e < E ? e : 0) * N + q * seg);
     const float xs = tok < T ? 1.0f : 0.0f, ws = e < E ? 1.0f : 0.0f;
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s = 0; s < seg / 4; s++) {
-        const float4 a = xr[s], b = wr[s];
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x * xs, b.x * ws, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y * xs, b.y * ws, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z * xs, b.z * ws, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w * xs, b.w * ws, acc, 0, 0, 0);
+    // four independent accumulators, each fed from its own float4 of the
+    // slice; 4 float4 of x and of Wr in flight per lane per step
+    v4f acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
+                  {0.0f, 0.0f, 0.0f, 0.0f}};
+    for (int s = 0; s < seg / 4; s += 4) {
+        float4 a[4], b[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            a[u] = xr[s + u];
+            b[u] = wr[s + u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x * xs, b[u].x * ws, acc[u], 0, 0, 0);
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y * xs, b[u].y * ws, acc[u], 0, 0, 0);
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z * xs, b[u].z * ws, acc[u], 0, 0, 0);
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w * xs, b[u].w * ws, acc[u], 0, 0, 0);
+        }
     }
+    const v4f sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     // lane holds logits[tb*16 + 4q + i][eb*16 + lane%16]
     const int eo = eb * 16 + (lane & 15);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int to = tb * 16 + 4 * q + i;
-        if (to < T && eo < E) logits[(size_t)to * E + eo] = bias ? acc[i] + bias[eo] : acc[i];
+        if (to < T && eo < E) logits[(size_t)to * E + eo] = bias ? sum[i] + bias[eo] : sum[i];
     }
 }
 
 // ---------------------------------------------------------------- group --
 // grp layout: cnt[E+1], off[E+2], tbo[E+2] (16-pair blocks per bucket,
-// prefix), then perm[T*S] (pair ids = t*S + slot, bucketed by expert).
-// Positions inside a bucket come from LDS atomics; every pair's result is
-// computed independently of its neighbours, so the order does not change
-// any output.
+// prefix); blk[b] = the bucket of global 16-pair block b; perm[T*S] (pair
+// ids = t*S + slot, bucketed by expert).  Positions inside a bucket come
+// from LDS atomics; every pair's result is computed independently of its
+// neighbours, so the order does not change any output.
 __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel, int T, int K, int E,
-                                                     int *__restrict__ grp, int *__restrict__ perm)
+                                                     int *__restrict__ grp, int *__restrict__ blk,
+                                                     int *__restrict__ perm)
 {
-    __shared__ int s_cnt[257], s_off[258], s_fill[257];
+    __shared__ int s_cnt[257], s_off[258], s_fill[257], s_inc[257], s_binc[257];
     const int tid = (int)threadIdx.x, S = K + 1;
     for (int e = tid; e <= E; e += 1024) {
         s_cnt[e] = 0;
@@ -91,19 +106,39 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
     for (int p = tid; p < T * K; p += 1024) atomicAdd(&s_cnt[expert(p)], 1);
     if (tid == 0) s_cnt[E] = T;      // shared expert: every token
     __syncthreads();
-    if (tid == 0) {
-        int o = 0, b = 0;
-        int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
-        for (int e = 0; e <= E; e++) {
-            s_off[e] = o;
-            cnt[e] = s_cnt[e];
-            off[e] = o;
-            tbo[e] = b;
-            o += s_cnt[e];
-            b += (s_cnt[e] + PB - 1) / PB;
+    // inclusive prefix sums of the pair counts and of the 16-pair block
+    // counts over the E + 1 buckets (Hillis-Steele in LDS, 9 steps)
+    if (tid <= E) {
+        s_inc[tid] = s_cnt[tid];
+        s_binc[tid] = (s_cnt[tid] + PB - 1) / PB;
+    }
+    __syncthreads();
+    for (int d = 1; d <= 256; d <<= 1) {
+        int a = 0, b = 0;
+        if (tid <= E && tid >= d) {
+            a = s_inc[tid - d];
+            b = s_binc[tid - d];
         }
-        off[E + 1] = o;
-        tbo[E + 1] = b;
+        __syncthreads();
+        if (tid <= E && tid >= d) {
+            s_inc[tid] += a;
+            s_binc[tid] += b;
+        }
+        __syncthreads();
+    }
+    if (tid <= E) {
+        int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
+        const int c = s_cnt[tid];
+        s_off[tid] = s_inc[tid] - c;
+        cnt[tid] = c;
+        off[tid] = s_inc[tid] - c;
+        const int nb = (c + PB - 1) / PB, b0 = s_binc[tid] - nb;
+        tbo[tid] = b0;
+        for (int i = 0; i < nb; i++) blk[b0 + i] = tid;
+        if (tid == E) {
+            off[E + 1] = s_inc[E];
+            tbo[E + 1] = s_binc[E];
+        }
     }
     __syncthreads();
     for (int p = tid; p < T * K; p += 1024) {
@@ -113,18 +148,11 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
     for (int t = tid; t < T; t += 1024) perm[s_off[E] + t] = t * S + K;
 }
 
-// block (bucket e, local block ltb) of a global 16-pair block index; -1 past the end
-__device__ __forceinline__ int find_bucket(const int *tbo, int E, int tbg)
-{
-    if (tbg >= tbo[E + 1]) return -1;
-    int lo = 0, hi = E;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tbo[mid] <= tbg) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
+// LDS row stride of the staged activations: 16 bytes of padding move each
+// row 4 banks on, so the 16 rows one MFMA operand read touches (8 bytes
+// each, 4 lane groups 8 bytes apart) fall on 64 distinct banks
+template <int NB>
+constexpr int arow() { return NB * QK_K + 16; }
 
 __device__ __forceinline__ long pack_nib(uint2 v, int hi)
 {
@@ -133,105 +161,128 @@ __device__ __forceinline__ long pack_nib(uint2 v, int hi)
 }
 
 // ------------------------------------------------------- Q4_K x Q8_K tile --
-// One wave: 16 weight rows (row lane%16 at wrow, consecutive super-blocks)
-// against the 16 staged activation rows; adds the fp32 results of pairs
-// 4*(lane/16)+i for row lane%16 into r[i].  All weight bytes of up to 8
-// super-blocks are requested before the first is used.  Activation staging
-// in LDS: aq[16][NB*256] int8, ad[NB][16] scales, as[NB*8][16] sub-block sums.
-template <int NB>
-__device__ __forceinline__ void q4k_tile(const uint8_t *wrow, const int8_t *aq, const float *ad,
-                                         const int *as, float (&r)[4])
+// One wave: 16 weight rows (row lane%16, consecutive super-blocks) against
+// the 16 staged activation rows; adds the fp32 results of pairs
+// 4*(lane/16)+i for row lane%16 into r[i].  The lane's weight bytes of CH
+// super-blocks are loaded into registers first (q4w_load, issued before the
+// activations are staged), then consumed (q4w_mma).  Activation staging in
+// LDS: aq[16][arow] int8, ad[NB][16] scales, as[NB*8][16] sub-block sums.
+template <int CH>
+struct Q4W {
+    uint4 hdr[CH];
+    uint2 qs[CH][4];
+};
+
+template <int CH>
+__device__ __forceinline__ void q4w_load(Q4W<CH> &w, const uint8_t *wrow, int c0)
 {
-    constexpr int CH = NB < 8 ? NB : 8;
+    const int q = lane_id() >> 4;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint8_t *blk = wrow + (size_t)(c0 + c) * Q4K_BYTES;
+        w.hdr[c] = ld16(blk);
+#pragma unroll
+        for (int g = 0; g < 4; g++) w.qs[c][g] = ld8(blk + 16 + 32 * g + 8 * q);
+    }
+}
+
+template <int NB, int CH>
+__device__ __forceinline__ void q4w_mma(const Q4W<CH> &w, int c0, const int8_t *aq, const float *ad,
+                                        float (&r)[4])
+{
     const int lane = lane_id(), lr = lane & 15, q = lane >> 4;
-    for (int c0 = 0; c0 < NB; c0 += CH) {
-        uint4 hdr[CH];
-        uint2 qs[CH][4];
 #pragma unroll
-        for (int c = 0; c < CH; c++) {
-            const uint8_t *blk = wrow + (size_t)(c0 + c) * Q4K_BYTES;
-            hdr[c] = ld16(blk);
+    for (int c = 0; c < CH; c++) {
+        const int ib = c0 + c;
+        // the 8 six-bit scales and mins of the block (src/q8k.c:22-30),
+        // packed one per byte: sub-blocks 0-3 and 4-7
+        const uint32_t y = w.hdr[c].y, z = w.hdr[c].z, x = w.hdr[c].w;
+        const uint32_t sc_lo = y & 0x3F3F3F3Fu, m_lo = z & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (x & 0x0F0F0F0Fu) | (((y >> 6) & 0x03030303u) << 4);
+        const uint32_t m_hi = ((x >> 4) & 0x0F0F0F0Fu) | (((z >> 6) & 0x03030303u) << 4);
+        int accs[4] = {0, 0, 0, 0};
+        // min term: sum over the block of m(sub-block of k) * xq[k] -- an
+        // MFMA against the mins broadcast over each sub-block, accumulated in
+        // the matrix core across the 8 sub-blocks (exact: int32)
+        v4i accm = {0, 0, 0, 0};
 #pragma unroll
-            for (int g = 0; g < 4; g++) qs[c][g] = ld8(blk + 16 + 32 * g + 8 * q);
+        for (int j = 0; j < 8; j++) {
+            const long a = *(const long *)(aq + lr * arow<NB>() + ib * QK_K + 32 * j + 8 * q);
+            const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, pack_nib(w.qs[c][j >> 1], j & 1),
+                                                                v4i{0, 0, 0, 0}, 0, 0, 0);
+            const int sc = (int)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 63);
+            const uint32_t mb = (((j < 4 ? m_lo : m_hi) >> (8 * (j & 3))) & 63) * 0x01010101u;
+            accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, (long)(((unsigned long long)mb << 32) | mb), accm, 0, 0, 0);
+            accs[0] += sc * p[0];
+            accs[1] += sc * p[1];
+            accs[2] += sc * p[2];
+            accs[3] += sc * p[3];
         }
-#pragma unroll
-        for (int c = 0; c < CH; c++) {
-            const int ib = c0 + c;
-            int accs[4] = {0, 0, 0, 0}, accm[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const long a = *(const long *)(aq + lr * (NB * QK_K) + ib * QK_K + 32 * j + 8 * q);
-                const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, pack_nib(qs[c][j >> 1], j & 1),
-                                                                    v4i{0, 0, 0, 0}, 0, 0, 0);
-                uint32_t sc, m;
-                q4_scale_min(j, hdr[c].y, hdr[c].z, hdr[c].w, sc, m);
-                const int4 xs = *(const int4 *)(as + (ib * 8 + j) * 16 + 4 * q);
-                accs[0] += (int)sc * p[0];
-                accs[1] += (int)sc * p[1];
-                accs[2] += (int)sc * p[2];
-                accs[3] += (int)sc * p[3];
-                accm[0] += (int)m * xs.x;
-                accm[1] += (int)m * xs.y;
-                accm[2] += (int)m * xs.z;
-                accm[3] += (int)m * xs.w;
-            }
-            const float d = h2f(hdr[c].x & 0xffff), dmin = h2f(hdr[c].x >> 16);
-            const float4 xd = *(const float4 *)(ad + ib * 16 + 4 * q);
-            r[0] += (d * xd.x) * (float)accs[0] - (dmin * xd.x) * (float)accm[0];
-            r[1] += (d * xd.y) * (float)accs[1] - (dmin * xd.y) * (float)accm[1];
-            r[2] += (d * xd.z) * (float)accs[2] - (dmin * xd.z) * (float)accm[2];
-            r[3] += (d * xd.w) * (float)accs[3] - (dmin * xd.w) * (float)accm[3];
-        }
+        const float d = h2f(w.hdr[c].x & 0xffff), dmin = h2f(w.hdr[c].x >> 16);
+        const float4 xd = *(const float4 *)(ad + ib * 16 + 4 * q);
+        r[0] += (d * xd.x) * (float)accs[0] - (dmin * xd.x) * (float)accm[0];
+        r[1] += (d * xd.y) * (float)accs[1] - (dmin * xd.y) * (float)accm[1];
+        r[2] += (d * xd.z) * (float)accs[2] - (dmin * xd.z) * (float)accm[2];
+        r[3] += (d * xd.w) * (float)accs[3] - (dmin * xd.w) * (float)accm[3];
     }
 }
 
 // ------------------------------------------------------- Q6_K x Q8_K tile --
-// Same contract for Q6_K rows (NB <= 4); one MFMA per 16-wide group, whose
-// 16 values sit in lanes q = 0, 1 (k 0..15); lanes q = 2, 3 carry zero
-// weights.  For (block, half n, lane half hl) a lane q < 2 holds the ql
-// bytes of quarters Q = 0/2 and 1/3 (low/high nibbles) and the qh bytes
-// shared by all four quarters, all requested before the first MFMA.
+// Same contract for Q6_K rows; one MFMA per 16-wide group, whose 16 values
+// sit in lanes q = 0, 1 (k 0..15); lanes q = 2, 3 carry zero weights.  For
+// (block, half n, lane half hl) a lane q < 2 holds the ql bytes of quarters
+// Q = 0/2 and 1/3 (low/high nibbles) and the qh bytes of all four.
 template <int NB>
-__device__ __forceinline__ void q6k_tile(const uint8_t *wrow, const int8_t *aq, const float *ad, float (&r)[4])
-{
-    const int lane = lane_id(), lr = lane & 15, q = lane >> 4, qq = q & 1;
+struct Q6W {
     uint2 ql[NB][2][2][2], qh[NB][2][2];     // [block][n][hl][Q & 1], [block][n][hl]
     uint4 sc16[NB];
     uint32_t dbits[NB];
+};
+
+template <int NB>
+__device__ __forceinline__ void q6w_load(Q6W<NB> &w, const uint8_t *wrow)
+{
+    const int q = lane_id() >> 4, qq = q & 1;
 #pragma unroll
     for (int ib = 0; ib < NB; ib++) {
         const uint8_t *blk = wrow + (size_t)ib * Q6K_BYTES;
-        sc16[ib] = ld16(blk + 192);
-        dbits[ib] = ld2(blk + 208);
+        w.sc16[ib] = ld16(blk + 192);
+        w.dbits[ib] = ld2(blk + 208);
 #pragma unroll
         for (int n = 0; n < 2; n++)
 #pragma unroll
             for (int hl = 0; hl < 2; hl++) {
                 const int l0 = 16 * hl + 8 * qq;
                 if (q < 2) {
-                    ql[ib][n][hl][0] = ld8(blk + 64 * n + l0);
-                    ql[ib][n][hl][1] = ld8(blk + 64 * n + 32 + l0);
-                    qh[ib][n][hl] = ld8(blk + 128 + 32 * n + l0);
+                    w.ql[ib][n][hl][0] = ld8(blk + 64 * n + l0);
+                    w.ql[ib][n][hl][1] = ld8(blk + 64 * n + 32 + l0);
+                    w.qh[ib][n][hl] = ld8(blk + 128 + 32 * n + l0);
                 } else {
-                    ql[ib][n][hl][0] = ql[ib][n][hl][1] = qh[ib][n][hl] = make_uint2(0, 0);
+                    w.ql[ib][n][hl][0] = w.ql[ib][n][hl][1] = w.qh[ib][n][hl] = make_uint2(0, 0);
                 }
             }
     }
+}
+
+template <int NB>
+__device__ __forceinline__ void q6w_mma(const Q6W<NB> &w, const int8_t *aq, const float *ad, float (&r)[4])
+{
+    const int lane = lane_id(), lr = lane & 15, q = lane >> 4, qq = q & 1;
 #pragma unroll
     for (int ib = 0; ib < NB; ib++) {
         int acc[4] = {0, 0, 0, 0};
-        const uint32_t scw[4] = {sc16[ib].x, sc16[ib].y, sc16[ib].z, sc16[ib].w};
+        const uint32_t scw[4] = {w.sc16[ib].x, w.sc16[ib].y, w.sc16[ib].z, w.sc16[ib].w};
 #pragma unroll
         for (int gg = 0; gg < 16; gg++) {
             // group gg = 8n + 2Q + hl: elements 128n + 32Q + 16hl + 0..15
             const int n = gg >> 3, Q = (gg >> 1) & 3, hl = gg & 1;
-            const uint2 l8 = ql[ib][n][hl][Q & 1], h8 = qh[ib][n][hl];
+            const uint2 l8 = w.ql[ib][n][hl][Q & 1], h8 = w.qh[ib][n][hl];
             const uint32_t lo0 = Q < 2 ? l8.x & 0x0F0F0F0Fu : (l8.x >> 4) & 0x0F0F0F0Fu;
             const uint32_t lo1 = Q < 2 ? l8.y & 0x0F0F0F0Fu : (l8.y >> 4) & 0x0F0F0F0Fu;
             const uint32_t hb0 = ((h8.x >> (2 * Q)) & 0x03030303u) << 4;
             const uint32_t hb1 = ((h8.y >> (2 * Q)) & 0x03030303u) << 4;
             const long b = q < 2 ? (long)(((unsigned long long)q6_center(lo1 | hb1) << 32) | q6_center(lo0 | hb0)) : 0;
-            const long a = *(const long *)(aq + lr * (NB * QK_K) + ib * QK_K + 128 * n + 32 * Q + 16 * hl + 8 * qq);
+            const long a = *(const long *)(aq + lr * arow<NB>() + ib * QK_K + 128 * n + 32 * Q + 16 * hl + 8 * qq);
             const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
             const int sc = (int)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 255);
             acc[0] += sc * p[0];
@@ -239,7 +290,7 @@ __device__ __forceinline__ void q6k_tile(const uint8_t *wrow, const int8_t *aq, 
             acc[2] += sc * p[2];
             acc[3] += sc * p[3];
         }
-        const float d = h2f(dbits[ib]);
+        const float d = h2f(w.dbits[ib]);
         const float4 xd = *(const float4 *)(ad + ib * 16 + 4 * q);
         r[0] += d * xd.x * (float)acc[0];
         r[1] += d * xd.y * (float)acc[1];
@@ -250,9 +301,11 @@ __device__ __forceinline__ void q6k_tile(const uint8_t *wrow, const int8_t *aq, 
 
 // Stage the Q8_K rows of the block's pairs into LDS (zeros for missing
 // pairs).  src rows are indexed by `row_of(pair)`; NB blocks of 256 each.
+// (The Q4_K min term is taken by the matrix core from the staged xq, so the
+// Q8_K group sums are not needed here.)
 template <int NB, typename RowOf>
 __device__ __forceinline__ void stage_q8k(const int *s_pair, RowOf row_of, const int8_t *xq, const float *xd,
-                                          const int16_t *xs, int8_t *aq, float *ad, int *as)
+                                          int8_t *aq, float *ad)
 {
     const int tid = (int)threadIdx.x;
     constexpr int L = NB * QK_K;
@@ -260,16 +313,11 @@ __device__ __forceinline__ void stage_q8k(const int *s_pair, RowOf row_of, const
         const int tok = c / (L / 16), part = c % (L / 16);
         const int pr = s_pair[tok];
         const uint4 v = pr >= 0 ? *(const uint4 *)(xq + (size_t)row_of(pr) * L + part * 16) : make_uint4(0, 0, 0, 0);
-        *(uint4 *)(aq + tok * L + part * 16) = v;
+        *(uint4 *)(aq + tok * arow<NB>() + part * 16) = v;
     }
     for (int c = tid; c < NB * PB; c += 256) {
         const int ib = c / PB, tok = c % PB, pr = s_pair[tok];
         ad[ib * PB + tok] = pr >= 0 ? xd[(size_t)row_of(pr) * NB + ib] : 0.0f;
-    }
-    for (int c = tid; c < NB * 8 * PB; c += 256) {
-        const int sub = c / PB, tok = c % PB, pr = s_pair[tok];
-        const int16_t *s = xs + (size_t)row_of(pr < 0 ? 0 : pr) * (L / 16) + 2 * sub;
-        as[sub * PB + tok] = pr >= 0 ? (int)s[0] + (int)s[1] : 0;
     }
 }
 
@@ -277,40 +325,48 @@ __device__ __forceinline__ void stage_q8k(const int *s_pair, RowOf row_of, const
 // grid: (max 16-pair blocks) x (F / 32); a workgroup = one pair block x 32
 // row pairs: waves 0-1 the gate rows, waves 2-3 the up rows (one weight
 // matrix per wave keeps all its bytes in flight at once), met in LDS for
-// h[pair][row] = silu(g) * u.
+// h[pair][row] = silu(g) * u.  The weight loads are issued before the
+// activations are staged.
 template <int NBE>
 __global__ __launch_bounds__(256, 2) void gateup_grouped_kernel(
     const uint8_t *__restrict__ gate_exps, const uint8_t *__restrict__ up_exps,
     const uint8_t *__restrict__ gate_sh, const uint8_t *__restrict__ up_sh, int E, int S, int F,
-    const int *__restrict__ grp, const int *__restrict__ perm, const int8_t *__restrict__ xq,
-    const float *__restrict__ xd, const int16_t *__restrict__ xs, float *__restrict__ h)
+    const int *__restrict__ grp, const int *__restrict__ blk, const int *__restrict__ perm,
+    const int8_t *__restrict__ xq, const float *__restrict__ xd, const int16_t *__restrict__ xs,
+    float *__restrict__ h)
 {
-    constexpr int N = NBE * QK_K;
-    __shared__ __align__(16) int8_t s_aq[PB * N];
+    constexpr int CH = NBE < 8 ? NBE : 8;
+    __shared__ __align__(16) int8_t s_aq[PB * arow<NBE>()];
     __shared__ __align__(16) float s_ad[NBE * PB];
-    __shared__ __align__(16) int s_as[NBE * 8 * PB];
     __shared__ float s_res[2][32][PB + 1];
     __shared__ int s_pair[PB];
     const int rblocks = F / 32;
     const int tbg = (int)blockIdx.x / rblocks, rb = (int)blockIdx.x % rblocks;
     const int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
-    const int e = find_bucket(tbo, E, tbg);
-    if (e < 0) return;
+    if (tbg >= tbo[E + 1]) return;
+    const int e = blk[tbg];
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), lr = lane & 15, q = lane >> 4;
+    const int mat = wv >> 1, lrow = 16 * (wv & 1) + lr;       // 0 gate / 1 up, row within the 32
+    const size_t rowb = (size_t)NBE * Q4K_BYTES;
+    const uint8_t *W = (mat == 0 ? (e < E ? gate_exps + (size_t)e * F * rowb : gate_sh)
+                                 : (e < E ? up_exps + (size_t)e * F * rowb : up_sh)) +
+                       (size_t)(rb * 32 + lrow) * rowb;
+    Q4W<CH> w;
+    q4w_load(w, W, 0);
     const int ltb = tbg - tbo[e];
     if (threadIdx.x < PB) {
         const int i = PB * ltb + (int)threadIdx.x;
         s_pair[threadIdx.x] = i < cnt[e] ? perm[off[e] + i] : -1;
     }
     __syncthreads();
-    stage_q8k<NBE>(s_pair, [&](int pr) { return pr / S; }, xq, xd, xs, s_aq, s_ad, s_as);
+    stage_q8k<NBE>(s_pair, [&](int pr) { return pr / S; }, xq, xd, s_aq, s_ad);
     __syncthreads();
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), lr = lane & 15, q = lane >> 4;
-    const int mat = wv >> 1, lrow = 16 * (wv & 1) + lr;       // 0 gate / 1 up, row within the 32
-    const size_t rowb = (size_t)NBE * Q4K_BYTES;
-    const uint8_t *W = mat == 0 ? (e < E ? gate_exps + (size_t)e * F * rowb : gate_sh)
-                                : (e < E ? up_exps + (size_t)e * F * rowb : up_sh);
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    q4k_tile<NBE>(W + (size_t)(rb * 32 + lrow) * rowb, s_aq, s_ad, s_as, r);
+    q4w_mma<NBE, CH>(w, 0, s_aq, s_ad, r);
+    for (int c0 = CH; c0 < NBE; c0 += CH) {
+        q4w_load(w, W, c0);
+        q4w_mma<NBE, CH>(w, c0, s_aq, s_ad, r);
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) s_res[mat][lrow][4 * q + i] = r[i];
     __syncthreads();
@@ -322,39 +378,57 @@ __global__ __launch_bounds__(256, 2) void gateup_grouped_kernel(
 }
 
 // ----------------------------------------------------------------- down --
-// grid: (max 16-pair blocks) x (N / 64); y[pair][row] = row . Q8_K(h[pair]).
+// grid: (max 16-pair blocks) x (N / 64); y[pair][row] = row . Q8_K(h[pair]),
+// 16 rows per wave; the weight loads are issued before the staging.
+template <int NBF, int TD>
+__device__ __forceinline__ void down_rows(const uint8_t *D, const int8_t *aq, const float *ad,
+                                          const int *s_pair, float (&r)[4])
+{
+    if constexpr (TD == QMAG_TYPE_Q6_K) {
+        Q6W<NBF> w;
+        q6w_load(w, D);
+        __syncthreads();          // the staging (issued by the caller) is complete
+        q6w_mma<NBF>(w, aq, ad, r);
+    } else {
+        Q4W<NBF> w;
+        q4w_load(w, D, 0);
+        __syncthreads();
+        q4w_mma<NBF, NBF>(w, 0, aq, ad, r);
+    }
+}
+
 template <int NBF>
 __global__ __launch_bounds__(256, 2) void down_grouped_kernel(
     const uint8_t *__restrict__ down_exps, int t_down, const uint8_t *__restrict__ down_sh, int t_down_sh,
-    int E, int N, const int *__restrict__ grp, const int *__restrict__ perm, const int8_t *__restrict__ hq,
-    const float *__restrict__ hd, const int16_t *__restrict__ hs, float *__restrict__ y)
+    int E, int N, const int *__restrict__ grp, const int *__restrict__ blk, const int *__restrict__ perm,
+    const int8_t *__restrict__ hq, const float *__restrict__ hd, const int16_t *__restrict__ hs,
+    float *__restrict__ y)
 {
-    constexpr int F = NBF * QK_K;
-    __shared__ __align__(16) int8_t s_aq[PB * F];
+    __shared__ __align__(16) int8_t s_aq[PB * arow<NBF>()];
     __shared__ __align__(16) float s_ad[NBF * PB];
-    __shared__ __align__(16) int s_as[NBF * 8 * PB];
     __shared__ int s_pair[PB];
     const int rblocks = N / 64;
     const int tbg = (int)blockIdx.x / rblocks, rb = (int)blockIdx.x % rblocks;
     const int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
-    const int e = find_bucket(tbo, E, tbg);
-    if (e < 0) return;
+    if (tbg >= tbo[E + 1]) return;
+    const int e = blk[tbg];
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), lr = lane & 15, q = lane >> 4;
+    const int row = rb * 64 + wv * 16 + lr;
     const int ltb = tbg - tbo[e];
     if (threadIdx.x < PB) {
         const int i = PB * ltb + (int)threadIdx.x;
         s_pair[threadIdx.x] = i < cnt[e] ? perm[off[e] + i] : -1;
     }
     __syncthreads();
-    stage_q8k<NBF>(s_pair, [&](int pr) { return pr; }, hq, hd, hs, s_aq, s_ad, s_as);
-    __syncthreads();
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), lr = lane & 15, q = lane >> 4;
-    const int row = rb * 64 + wv * 16 + lr;
+    // the staging loads go out first; each wave then issues its weight
+    // loads and waits at the barrier inside down_rows
+    stage_q8k<NBF>(s_pair, [&](int pr) { return pr; }, hq, hd, s_aq, s_ad);
     const int td = e < E ? t_down : t_down_sh;
     const size_t rowb = (size_t)NBF * (td == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES);
     const uint8_t *D = (e < E ? down_exps + (size_t)e * N * rowb : down_sh) + row * rowb;
     float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (td == QMAG_TYPE_Q6_K) q6k_tile<NBF>(D, s_aq, s_ad, r);
-    else q4k_tile<NBF>(D, s_aq, s_ad, s_as, r);
+    if (td == QMAG_TYPE_Q6_K) down_rows<NBF, QMAG_TYPE_Q6_K>(D, s_aq, s_ad, s_pair, r);
+    else down_rows<NBF, QMAG_TYPE_Q4_K>(D, s_aq, s_ad, s_pair, r);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int pr = s_pair[4 * q + i];
@@ -388,21 +462,21 @@ int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *lo
 }
 
 template <int NBE>
-static void launch_gu(const qmag_moe_layer *L, int S, int max_blocks, const int *grp, const int *perm,
-                      const int8_t *xq, const float *xd, const int16_t *xs, float *h, hipStream_t s)
+static void launch_gu(const qmag_moe_layer *L, int S, int max_blocks, const int *grp, const int *blk,
+                      const int *perm, const int8_t *xq, const float *xd, const int16_t *xs, float *h, hipStream_t s)
 {
     hipLaunchKernelGGL(gateup_grouped_kernel<NBE>, dim3(max_blocks * (L->n_ff / 32)), dim3(256), 0, s,
                        (const uint8_t *)L->gate_exps, (const uint8_t *)L->up_exps, (const uint8_t *)L->gate_shexp,
-                       (const uint8_t *)L->up_shexp, L->n_expert, S, L->n_ff, grp, perm, xq, xd, xs, h);
+                       (const uint8_t *)L->up_shexp, L->n_expert, S, L->n_ff, grp, blk, perm, xq, xd, xs, h);
 }
 
 template <int NBF>
-static void launch_dn(const qmag_moe_layer *L, int max_blocks, const int *grp, const int *perm,
-                      const int8_t *hq, const float *hd, const int16_t *hs, float *y, hipStream_t s)
+static void launch_dn(const qmag_moe_layer *L, int max_blocks, const int *grp, const int *blk,
+                      const int *perm, const int8_t *hq, const float *hd, const int16_t *hs, float *y, hipStream_t s)
 {
     hipLaunchKernelGGL(down_grouped_kernel<NBF>, dim3(max_blocks * (L->n_embd / 64)), dim3(256), 0, s,
                        (const uint8_t *)L->down_exps, L->t_down_exps, (const uint8_t *)L->down_shexp,
-                       L->t_down_shexp, L->n_expert, L->n_embd, grp, perm, hq, hd, hs, y);
+                       L->t_down_shexp, L->n_expert, L->n_embd, grp, blk, perm, hq, hd, hs, y);
 }
 
 int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, const float *gs,
@@ -411,24 +485,24 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
 {
     const int N = L->n_embd, F = L->n_ff, E = L->n_expert, K = L->n_used, S = K + 1;
     int st;
-    int *grp = (int *)workspace(WS_GRP, sizeof(int) * ((size_t)3 * (E + 2) + (size_t)T * S), &st);
-    if (st) return st;
-    int *perm = grp + 3 * (E + 2);
-    float *y = (float *)workspace(WS_Y, sizeof(float) * (size_t)T * S * N, &st);
-    if (st) return st;
     // an upper bound of the 16-pair blocks: sum ceil(n_e / 16) <= T*K/16 + E, plus the shared bucket
     const int max_blocks = (T * K + PB - 1) / PB + E + (T + PB - 1) / PB;
+    int *grp = (int *)workspace(WS_GRP, sizeof(int) * ((size_t)3 * (E + 2) + max_blocks + (size_t)T * S), &st);
+    if (st) return st;
+    int *blk = grp + 3 * (E + 2), *perm = blk + max_blocks;
+    float *y = (float *)workspace(WS_Y, sizeof(float) * (size_t)T * S * N, &st);
+    if (st) return st;
 
     prof_begin(PROF_GROUP, s);
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, sel, T, K, E, grp, perm);
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, sel, T, K, E, grp, blk, perm);
     prof_end(PROF_GROUP, s);
     prof_begin(PROF_GATEUP, s);
     switch (N / QK_K) {
-    case 1: launch_gu<1>(L, S, max_blocks, grp, perm, xq, xd, xs, h, s); break;
-    case 2: launch_gu<2>(L, S, max_blocks, grp, perm, xq, xd, xs, h, s); break;
-    case 4: launch_gu<4>(L, S, max_blocks, grp, perm, xq, xd, xs, h, s); break;
-    case 8: launch_gu<8>(L, S, max_blocks, grp, perm, xq, xd, xs, h, s); break;
-    default: launch_gu<16>(L, S, max_blocks, grp, perm, xq, xd, xs, h, s); break;
+    case 1: launch_gu<1>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
+    case 2: launch_gu<2>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
+    case 4: launch_gu<4>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
+    case 8: launch_gu<8>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
+    default: launch_gu<16>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
     }
     prof_end(PROF_GATEUP, s);
     prof_begin(PROF_HQUANT, s);
@@ -437,9 +511,9 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
     if (st) return st;
     prof_begin(PROF_DOWN, s);
     switch (F / QK_K) {
-    case 1: launch_dn<1>(L, max_blocks, grp, perm, hq, hd, hs, y, s); break;
-    case 2: launch_dn<2>(L, max_blocks, grp, perm, hq, hd, hs, y, s); break;
-    default: launch_dn<4>(L, max_blocks, grp, perm, hq, hd, hs, y, s); break;
+    case 1: launch_dn<1>(L, max_blocks, grp, blk, perm, hq, hd, hs, y, s); break;
+    case 2: launch_dn<2>(L, max_blocks, grp, blk, perm, hq, hd, hs, y, s); break;
+    default: launch_dn<4>(L, max_blocks, grp, blk, perm, hq, hd, hs, y, s); break;
     }
     prof_end(PROF_DOWN, s);
     prof_begin(PROF_COMBINE, s);
