@@ -462,7 +462,11 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             TR(2);
 
             // ---- this wave's down rows of every slot into registers, and
-            // the next layer's router rows (this layer's are consumed)
+            // the next layer's router rows (this layer's are consumed).
+            // They are needed only after Q8_K(h): a short pause first lets
+            // the stream workgroups' gate/up requests, issued at the same
+            // moment, go out ahead of them.
+            __builtin_amdgcn_s_sleep(24);
             DRaw<TD> dr[DN_ROUNDS];
 #pragma unroll
             for (int j = 0; j < DN_ROUNDS; j++) {
