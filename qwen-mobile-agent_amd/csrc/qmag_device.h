@@ -23,15 +23,17 @@ __device__ __forceinline__ float h2f(uint32_t h16)
 // ------------------------------------------------------------ reductions --
 // All-reduce over aligned groups of W lanes (W = 4, 8, 16, 32, 64) using DPP
 // quad permutes, row mirrors and the gfx950 permlane swaps; no LDS traffic.
+// Every pattern used reads a valid lane of the same row, so the move can be
+// folded into the consuming add/max (one v_add_f32_dpp per step).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v)
 {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v)
 {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
 constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
@@ -111,6 +113,24 @@ __device__ __forceinline__ float group_min(float v)
 }
 
 template <int W>
+__device__ __forceinline__ int group_max_i(int v)
+{
+    if constexpr (W >= 2) v = max(v, dpp_i<DPP_XOR1>(v));
+    if constexpr (W >= 4) v = max(v, dpp_i<DPP_XOR2>(v));
+    if constexpr (W >= 8) v = max(v, dpp_i<DPP_HALF_MIRROR>(v));
+    if constexpr (W >= 16) v = max(v, dpp_i<DPP_MIRROR>(v));
+    if constexpr (W >= 32) {
+        auto p = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = max((int)p[0], (int)p[1]);
+    }
+    if constexpr (W >= 64) {
+        auto p = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+        v = max((int)p[0], (int)p[1]);
+    }
+    return v;
+}
+
+template <int W>
 __device__ __forceinline__ int group_min_i(int v)
 {
     if constexpr (W >= 2) v = min(v, dpp_i<DPP_XOR1>(v));
@@ -131,32 +151,47 @@ __device__ __forceinline__ int group_min_i(int v)
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
 // --------------------------------------------------------------- loads ----
-// Byte-addressed loads.  Q6_K super-blocks are 210 B, so odd blocks sit at
-// 2-byte alignment; gfx9 global memory runs in unaligned mode and these
-// compile to single global_load_dword{,x2,x4}.
+// Byte-addressed loads of weights and activations in HBM.  Q6_K
+// super-blocks are 210 B, so odd blocks sit at 2-byte alignment; gfx9 global
+// memory runs in unaligned mode and these compile to single
+// global_load_dword{,x2,x4}.  The pointers are cast to the global address
+// space explicitly: a pointer read from memory (a layer table) would
+// otherwise stay generic, and a flat load also counts against lgkmcnt, so
+// every later wait for an LDS read would wait for the weight load as well.
+typedef uint32_t g_u32x4 __attribute__((ext_vector_type(4), aligned(1)));
+typedef uint32_t g_u32x2 __attribute__((ext_vector_type(2), aligned(1)));
+typedef uint32_t g_u32 __attribute__((aligned(1)));
+typedef uint16_t g_u16 __attribute__((aligned(1)));
+#define QMAG_GLOBAL __attribute__((address_space(1)))
 __device__ __forceinline__ uint4 ld16(const uint8_t *p)
 {
-    uint4 v;
-    __builtin_memcpy(&v, p, 16);
-    return v;
+    const g_u32x4 v = *(const QMAG_GLOBAL g_u32x4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint2 ld8(const uint8_t *p)
 {
-    uint2 v;
-    __builtin_memcpy(&v, p, 8);
-    return v;
+    const g_u32x2 v = *(const QMAG_GLOBAL g_u32x2 *)p;
+    return make_uint2(v.x, v.y);
 }
 __device__ __forceinline__ uint32_t ld4(const uint8_t *p)
 {
-    uint32_t v;
-    __builtin_memcpy(&v, p, 4);
-    return v;
+    return *(const QMAG_GLOBAL g_u32 *)p;
 }
 __device__ __forceinline__ uint32_t ld2(const uint8_t *p)
 {
-    uint16_t v;
-    __builtin_memcpy(&v, p, 2);
-    return v;
+    return *(const QMAG_GLOBAL g_u16 *)p;
+}
+// naturally aligned scalar / float4 of an array in HBM, through a global pointer
+template <typename T>
+__device__ __forceinline__ T ldg(const T *p)
+{
+    return *(const QMAG_GLOBAL T *)p;
+}
+typedef float g_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ldg4(const float *p)
+{
+    const g_f32x4 v = *(const QMAG_GLOBAL g_f32x4 *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
@@ -196,6 +231,40 @@ __device__ __forceinline__ Q8Lane q8k_quant_lane(float4 v)
     r.packed = (uint32_t)(q0 & 255) | ((uint32_t)(q1 & 255) << 8) | ((uint32_t)(q2 & 255) << 16) |
                ((uint32_t)(q3 & 255) << 24);
     r.gsum = group_sum_i<4>(q0 + q1 + q2 + q3);
+    return r;
+}
+
+// The same quantisation with a 256-block spread over 32 lanes, 8 values per
+// lane (a = values 8L..8L+3, b = 8L+4..8L+7): each half of a wave quantises
+// its own block, with the same results as q8k_quant_lane.  gsum is the sum of
+// the 16-value group of the lane pair (2j, 2j+1).
+struct Q8Lane2 {
+    uint32_t packed[2];
+    float d;
+    int gsum;
+};
+
+__device__ __forceinline__ uint32_t q8_pack4(float4 v, float inv, int &sum)
+{
+    const int q0 = q8_round(v.x * inv), q1 = q8_round(v.y * inv);
+    const int q2 = q8_round(v.z * inv), q3 = q8_round(v.w * inv);
+    sum += q0 + q1 + q2 + q3;
+    return (uint32_t)(q0 & 255) | ((uint32_t)(q1 & 255) << 8) | ((uint32_t)(q2 & 255) << 16) |
+           ((uint32_t)(q3 & 255) << 24);
+}
+
+__device__ __forceinline__ Q8Lane2 q8k_quant_half(float4 a, float4 b)
+{
+    float m = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    const float amax = group_max<32>(m);
+    Q8Lane2 r;
+    r.d = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / r.d;
+    int s = 0;
+    r.packed[0] = q8_pack4(a, inv, s);
+    r.packed[1] = q8_pack4(b, inv, s);
+    r.gsum = group_sum_i<2>(s);
     return r;
 }
 

@@ -9,14 +9,17 @@
 //   core workgroups 0..127 (16 per XCD) each own 16 rows of the hidden state.
 //     They compute the router logits (2 per workgroup, router rows staged in
 //     LDS one layer ahead), Q8_K(x) (workgroups 0..7, one 256-block each,
-//     with that block's share of the shared-expert gate input) and the down
-//     projection + combine + residual of their rows for all 9 slots, with
-//     the down rows fetched into registers as soon as the selection is known.
+//     with that block's share of the shared-expert gate input) and the
+//     combine + residual of their rows from the 9 slots' down outputs.
 //   stream workgroups 128..511 (1536 waves) compute the gate/up row pairs:
 //     slot s < n_used is routed expert sel[s], slot n_used the shared one,
-//     three row pairs per wave; afterwards 18 of their waves quantise one
-//     h block each (a wave's loads complete in order, so pollers are kept
-//     out of the waves that hold prefetches in flight).
+//     three row pairs per wave.  Then 32 of them per slot (288 for 9 slots)
+//     run that slot's down projection over 64 rows each: gather the slot's
+//     h, quantise it (Q8_K(h), two blocks, in LDS) and take the dots of
+//     their down rows, which were fetched into registers as soon as the
+//     selection was known.  Spreading the down dots over 288 workgroups,
+//     each needing one slot's h, keeps both the gathers and the integer
+//     work per workgroup small.
 //
 // Hand-offs of one layer (each a set of tagged words, see below):
 //   x_l rows      core -> core            (2048 words, read by 128 workgroups)
@@ -25,8 +28,10 @@
 //                 needs no further hop
 //   Q8_K(x)       core 0..7 -> stream     (656 words, 8 replicas; produced
 //                 together with the logits, off the critical path)
-//   h             stream -> 18 quantiser waves
-//   Q8_K(h)       quantiser -> core       (1458 words, read by 128 workgroups)
+//   h             stream -> stream        (512 words of one slot, read by that
+//                                          slot's 32 down workgroups)
+//   y             stream -> core          (down outputs, 16 rows x 9 slots
+//                                          read by each core workgroup)
 //
 // Every published value is one 64-bit word {32 data bits, 32-bit tag},
 // written with a single-copy-atomic device-scope store; the tag is
@@ -57,8 +62,10 @@ constexpr int WROWS = CROWS / 4;                  // 4 per core wave
 constexpr int NLOG = 256 / CORE;                  // 2 router logits per core workgroup
 constexpr int GU_WAVES = (WGS - CORE) * 4;        // 1536 gate/up waves
 constexpr int MAX_RP = (SMAX * F + GU_WAVES - 1) / GU_WAVES;   // 3 row pairs per wave
-constexpr int DN_TASKS = WROWS * SMAX;            // (row, slot) pairs per core wave: 36
-constexpr int DN_ROUNDS = (DN_TASKS + 7) / 8;     // 8 lanes per pair: 5 rounds
+constexpr int DROWS = 64;                         // down rows per down workgroup (one slot)
+constexpr int DWG_PER_SLOT = N / DROWS;           // 32
+constexpr int DN_ROUNDS = DROWS / 4 / 8;          // 16 rows per wave, 8 lanes per row: 2 rounds
+static_assert(CORE + SMAX * DWG_PER_SLOT <= WGS, "down workgroups out of range");
 constexpr long SPIN_LIMIT = 1L << 22;
 
 // Q8_K records are laid out exactly as the LDS copy their readers keep, so a
@@ -66,31 +73,24 @@ constexpr long SPIN_LIMIT = 1L << 22;
 //   Q8_K(x): 512 packed xq words (block b at 64b), 8 scales d, 128 group
 //   sums, 8 partials of the shared-expert gate input (nn.c:452-454)
 constexpr int XR_D = N / 4, XR_S = XR_D + NBE, XR_G = XR_S + N / 16, XR_WORDS = XR_G + NBE;   // 656
-//   Q8_K(h), 2*SMAX blocks: packed words, scales (block k's scale is the
-//   word its readers poll first), group sums
-constexpr int HBLK = SMAX * NBF;                  // 18
-constexpr int HR_D = HBLK * 64, HR_S = HR_D + HBLK, HR_WORDS = HR_S + HBLK * 16;            // 1458
-constexpr int HQ_PAIRS_PER_THREAD = (HR_WORDS / 2 + 255) / 256;   // 3
-static_assert(HR_D % 2 == 0 && HR_S % 2 == 0 && HR_WORDS % 2 == 0, "Q8_K(h) record ranges must be even");
+//   Q8_K(h) of one slot in a down workgroup's LDS, 2 blocks: packed words,
+//   scales, group sums
+constexpr int HS_D = F / 4, HS_S = HS_D + NBF, HS_WORDS = HS_S + F / 16;                    // 162
 constexpr int REP = 8;                            // replicas of the widely read records
-// h block k (k < 2*SMAX) is quantised by wave 1 of stream workgroup
-// QWG0 + k*QWG_STEP, after that wave's own gate/up rows (odd step: the
-// quantisers spread over the 8 XCDs, which take workgroups round-robin)
-constexpr int QWG0 = CORE + 3, QWG_STEP = 21;
-static_assert(QWG0 + QWG_STEP * (2 * SMAX - 1) < WGS, "quantiser workgroups out of range");
 
 struct Tagged {
     unsigned long long logits[REP][256];          // logit e at word logit_pos(e)
     unsigned long long xq[REP][XR_WORDS];
     unsigned long long x[N];
-    unsigned long long h[SMAX * F];
-    unsigned long long hq[HR_WORDS + 14];         // padded to a multiple of 16 words
+    unsigned long long h[SMAX * F];               // slot s, row i at s*F + i
+    unsigned long long y[SMAX * N];               // down output of slot s, row r at s*N + r
 };
 // word offsets of the arrays (every array starts on a 16-byte boundary)
 constexpr int TW_LOGITS = 0, TW_XQ = TW_LOGITS + REP * 256, TW_X = TW_XQ + REP * XR_WORDS,
-              TW_H = TW_X + N, TW_HQ = TW_H + SMAX * F;
+              TW_H = TW_X + N, TW_Y = TW_H + SMAX * F;
 static_assert(offsetof(Tagged, xq) == 8 * TW_XQ && offsetof(Tagged, x) == 8 * TW_X &&
-              offsetof(Tagged, h) == 8 * TW_H && offsetof(Tagged, hq) == 8 * TW_HQ && XR_WORDS % 2 == 0,
+              offsetof(Tagged, h) == 8 * TW_H && offsetof(Tagged, y) == 8 * TW_Y && XR_WORDS % 2 == 0 &&
+              XR_G % 2 == 0 && TW_H % 2 == 0 && TW_Y % 2 == 0 && F % 2 == 0,
               "tagged layout");
 // Logits are stored so that the 16-byte pair p of lane l (p = l, l + 64)
 // holds experts l + 64h + 128(p >= 64), h = the half: a lane then reads
@@ -100,10 +100,6 @@ __device__ __forceinline__ int logit_pos(int e) { return 2 * ((e & 63) + 64 * (e
 __device__ __forceinline__ unsigned long long ld64(const unsigned long long *p)
 {
     return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st64(unsigned long long *p, uint32_t v, uint32_t seq)
-{
-    __hip_atomic_store(p, ((unsigned long long)seq << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // wait until all of this wave's outstanding memory operations completed
 __device__ __forceinline__ void drain() { __builtin_amdgcn_s_waitcnt(0); }
@@ -149,7 +145,19 @@ __device__ bool poll(const unsigned long long *p, Idx idx, uint32_t seq, uint32_
 // pair needs no atomicity as a whole; 16-byte loads halve the requests,
 // which is what bounds a workgroup's bulk read rate.
 constexpr int CPOL_SC1 = 16;
+constexpr int OOB_BYTE = 1 << 30;                 // beyond the Tagged buffer's records
 typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Publish one tagged word (index `word` of the Tagged buffer): an aligned
+// 8-byte vector store with the device-coherent policy, the instruction a
+// relaxed agent-scope atomic store compiles to.  Addressed through the
+// buffer resource so the only per-lane state is a 32-bit offset.
+__device__ __forceinline__ void st64(Rsrc rs, int word, uint32_t v, uint32_t seq)
+{
+    const u32x2 d = {v, seq};
+    __builtin_amdgcn_raw_buffer_store_b64(d, rs, word * 8, 0, CPOL_SC1);
+}
 
 // One wave reads CNT word pairs per lane.  code(k) = pair index * 4 + need
 // (need: bit 0 the low word, bit 1 the high word must carry seq), or -1 for
@@ -164,15 +172,30 @@ __device__ bool pollq(Rsrc rs, int base_word, Code code, uint32_t seq, uint32_t 
     for (int k = 0; k < CNT; k++)
         if (code(k) >= 0) pending |= 1u << k;
     for (long it = 0; it < SPIN_LIMIT; it++) {
+        // one batch of loads, then the checks: a round costs one memory
+        // latency, not one per pair.  A pair that is done or absent reads
+        // beyond the end of the buffer, which returns zeros without a memory
+        // access, so the loads need no branch.
+        decltype(__builtin_amdgcn_raw_buffer_load_b128(rs, 0, 0, 0)) v[CNT];
+#pragma unroll
+        for (int k = 0; k < CNT; k++) {
+            const int off = (pending & (1u << k)) ? (base_word + 2 * (code(k) >> 2)) * 8 : OOB_BYTE;
+            v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, CPOL_SC1);
+        }
+        // keep the batch together: without these the compiler sinks each load
+        // into the branch that checks it, or hoists a check between the
+        // loads, one memory latency per pair again
+        __asm__ volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < CNT; k++) __asm__ volatile("" : "+v"(v[k]));
 #pragma unroll
         for (int k = 0; k < CNT; k++) {
             if (pending & (1u << k)) {
                 const int c = code(k);
-                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (base_word + 2 * (c >> 2)) * 8, 0, CPOL_SC1);
-                const bool lo = !(c & 1) || v[1] == seq, hi = !(c & 2) || v[3] == seq;
+                const bool lo = !(c & 1) || v[k][1] == seq, hi = !(c & 2) || v[k][3] == seq;
                 if (lo && hi) {
-                    val[k][0] = v[0];
-                    val[k][1] = v[2];
+                    val[k][0] = v[k][0];
+                    val[k][1] = v[k][2];
                     pending &= ~(1u << k);
                 }
             }
@@ -318,9 +341,10 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
     __shared__ float4 s_x[N / 4];                 // core: x_l
     __shared__ float4 s_wr[NLOG][N / 4];          // core: this workgroup's router rows
     __shared__ uint4 s_xrec[(XR_WORDS + 3) / 4];  // stream: the Q8_K(x_l) record
-    __shared__ uint4 s_hrec[(HR_WORDS + 3) / 4];  // core: the Q8_K(h) record, all slots
+    __shared__ float4 s_hs[F / 4];                // down: h of the slot
+    __shared__ uint4 s_hq[(HS_WORDS + 3) / 4];    // down: Q8_K of that h
     __shared__ float s_gsp[NBE];                  // core: shared-gate input partials
-    __shared__ float s_dres[CROWS][SMAX + 1];     // core: per (row, slot) down dots
+    __shared__ float s_dres[CROWS][SMAX + 1];     // core: per (row, slot) down outputs
     __shared__ float s_xout[CROWS];               // core: x_{l+1} rows to publish
     __shared__ int s_sel[8];
     __shared__ float s_w[8];
@@ -361,7 +385,6 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
         // rows r0 .. r0+15; wave wv owns r0+4wv .. +3, lane i < 4 keeps the
         // residual value of row r0 + 4wv + i
         const int r0 = b * CROWS;
-        const int dq = lane & 7, dg = lane >> 3;      // down task: sub-task, lane group
         // the router rows of layer l go straight into LDS one layer ahead
         // (layer 0's here, layer l+1's once layer l's logits are computed)
         auto load_router_rows = [&](const qmag_moe_layer &Ln) {
@@ -422,24 +445,24 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                         s += w.x * a.x + w.y * a.y + w.z * a.z + w.w * a.w;
                     }
                     s = group_sum<64>(s);
-                    if (L.router_bias) s += L.router_bias[e];
-                    if (lane < REP) st64(tg->logits[lane] + logit_pos(e), __float_as_uint(s), seq);
+                    if (L.router_bias) s += ldg(L.router_bias + e);
+                    if (lane < REP) st64(rs, TW_LOGITS + lane * 256 + logit_pos(e), __float_as_uint(s), seq);
                     if (last && lane == 0) g_logits[e] = s;
                 }
             } else if (wv == 2 && b < NBE) {
                 const Q8Lane q = q8k_quant_lane(s_x[b * 64 + lane]);
-                const float4 wsh = ((const float4 *)L.gate_inp_shexp)[b * 64 + lane];
+                const float4 wsh = ldg4(L.gate_inp_shexp + 4 * (b * 64 + lane));
                 const int8_t *q8 = (const int8_t *)&q.packed;
                 float g = wsh.x * (float)q8[0] * q.d + wsh.y * (float)q8[1] * q.d +
                           wsh.z * (float)q8[2] * q.d + wsh.w * (float)q8[3] * q.d;
                 g = group_sum<64>(g);
 #pragma nounroll
                 for (int r = 0; r < REP; r++) {
-                    unsigned long long *o = tg->xq[r];
-                    st64(o + b * 64 + lane, q.packed, seq);
-                    if ((lane & 3) == 0) st64(o + XR_S + b * 16 + (lane >> 2), (uint32_t)q.gsum, seq);
-                    if (lane == 0) st64(o + XR_D + b, __float_as_uint(q.d), seq);
-                    if (lane == 1) st64(o + XR_G + b, __float_as_uint(g), seq);
+                    const int o = TW_XQ + r * XR_WORDS;
+                    st64(rs, o + b * 64 + lane, q.packed, seq);
+                    if ((lane & 3) == 0) st64(rs, o + XR_S + b * 16 + (lane >> 2), (uint32_t)q.gsum, seq);
+                    if (lane == 0) st64(rs, o + XR_D + b, __float_as_uint(q.d), seq);
+                    if (lane == 1) st64(rs, o + XR_G + b, __float_as_uint(g), seq);
                 }
             } else if (wv == 3) {
                 // ---- all logits -> softmax, top-K (wave 3 has stored nothing
@@ -461,67 +484,33 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             if (!wg_all(ok, s_vote, 1)) return;
             TR(2);
 
-            // ---- this wave's down rows of every slot into registers, and
-            // the next layer's router rows (this layer's are consumed).
-            // They are needed only after Q8_K(h): a short pause first lets
-            // the stream workgroups' gate/up requests, issued at the same
-            // moment, go out ahead of them.
-            __builtin_amdgcn_s_sleep(24);
-            DRaw<TD> dr[DN_ROUNDS];
-#pragma unroll
-            for (int j = 0; j < DN_ROUNDS; j++) {
-                d_zero(dr[j]);
-                const int t = 8 * j + dg;                // (row, slot) pair: row t & 3, slot t >> 2
-                if (t < WROWS * S) {
-                    const int slot = t >> 2, row = r0 + WROWS * wv + (t & 3);
-                    const uint8_t *slab = slot < K ? (const uint8_t *)L.down_exps + (size_t)s_sel[slot] * DN_SLAB
-                                                   : (const uint8_t *)L.down_shexp;
-                    d_load<TD>(dr[j], slab, row, dq);
-                }
-            }
+            // ---- the next layer's router rows (this layer's are consumed)
             if (!last) load_router_rows(layers[l + 1]);
             TR(3);
 
-            // ---- wave 0: the 2S block sentinels and the 8 shared-gate partials
-            if (wv == 0) {
-                uint32_t v[1];
-                const unsigned long long *src = lane < 32 ? tg->hq : tg->xq[rep];
-                ok = poll<1>(src, [&](int) {
-                    return lane < 2 * S ? HR_D + lane : (lane >= 32 && lane < 32 + NBE) ? XR_G + lane - 32 : -1;
-                }, seq, v, abort_flag);
-                if (lane >= 32 && lane < 32 + NBE) s_gsp[lane - 32] = __uint_as_float(v[0]);
-            }
-            if (!wg_all(ok, s_vote, 2)) return;
-            {
-                // word pairs; the used ranges start and end on even words
-                uint32_t v[HQ_PAIRS_PER_THREAD][2];
-                auto hp = [&](int k) {
-                    const int p = tid + 256 * k, i = 2 * p;
-                    const bool used = i < HR_D ? i < 2 * S * 64 : i < HR_S ? i < HR_D + 2 * S : i < HR_S + 2 * S * 16;
-                    return used ? 4 * p + 3 : -1;
+            // ---- the down outputs of this workgroup's rows, every slot
+            // (thread t < 8S: slot t/8, rows r0 + 2(t%8) + {0,1}), and the 8
+            // shared-gate partials (4 more pairs)
+            if (wv < 2) {
+                uint32_t v[1][2];
+                auto yp = [&](int) {
+                    if (tid < 8 * S) return 4 * ((TW_Y + (tid >> 3) * N + r0) / 2 + (tid & 7)) + 3;
+                    if (tid < 8 * S + NBE / 2) return 4 * ((TW_XQ + rep * XR_WORDS + XR_G) / 2 + tid - 8 * S) + 3;
+                    return -1;
                 };
-                ok = pollq<HQ_PAIRS_PER_THREAD>(rs, TW_HQ, hp, seq, v, abort_flag);
-#pragma unroll
-                for (int k = 0; k < HQ_PAIRS_PER_THREAD; k++)
-                    if (hp(k) >= 0) ((uint2 *)s_hrec)[hp(k) >> 2] = make_uint2(v[k][0], v[k][1]);
-            }
-            if (!wg_all(ok, s_vote, 3)) return;
-            TR(5);
-
-            // ---- down dots, then combine in the reference order (nn.c:614-629)
-#pragma unroll
-            for (int j = 0; j < DN_ROUNDS; j++) {
-                const int t = 8 * j + dg;
-                if (8 * j < WROWS * S) {                 // wave-uniform
-                    const int slot = t < WROWS * S ? t >> 2 : 0;
-                    float v = d_dot<TD>(dr[j], (const uint32_t *)s_hrec + slot * (F / 4),
-                                        (const float *)s_hrec + HR_D + slot * NBF,
-                                        (const int *)s_hrec + HR_S + slot * (F / 16), dq);
-                    v = group_sum<8>(v);
-                    if (dq == 0 && t < WROWS * S) s_dres[WROWS * wv + (t & 3)][slot] = v;
+                ok = pollq<1>(rs, 0, yp, seq, v, abort_flag);
+                if (tid < 8 * S) {
+                    s_dres[2 * (tid & 7)][tid >> 3] = __uint_as_float(v[0][0]);
+                    s_dres[2 * (tid & 7) + 1][tid >> 3] = __uint_as_float(v[0][1]);
+                } else if (tid < 8 * S + NBE / 2) {
+                    s_gsp[2 * (tid - 8 * S)] = __uint_as_float(v[0][0]);
+                    s_gsp[2 * (tid - 8 * S) + 1] = __uint_as_float(v[0][1]);
                 }
             }
-            __syncthreads();
+            if (!wg_all(ok, s_vote, 2)) return;
+            TR(4);
+
+            // ---- combine in the reference order (nn.c:614-629)
             if (lane < WROWS) {
                 float g = 0.0f;
 #pragma unroll
@@ -542,19 +531,20 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             __syncthreads();
             // wave 3 publishes the workgroup's 16 rows with one store
             if (!out && wv == 3 && lane < CROWS) {
-                if (!last) st64(tg->x + r0 + lane, __float_as_uint(s_xout[lane]), seq + 1u);
+                if (!last) st64(rs, TW_X + r0 + lane, __float_as_uint(s_xout[lane]), seq + 1u);
                 else x[r0 + lane] = s_xout[lane];
             }
             TR(6);
         }
     } else {
         // ============================================================== stream
-        const int gwv = (b - CORE) * 4 + wv;
+        const int sb = b - CORE, gwv = sb * 4 + wv;
         const int half = lane >> 5, l32 = lane & 31;
         const int gib = l32 >> 2, gg = l32 & 3;       // gate/up task: block, 64-lane group
-        // wave 1 of workgroup QWG0 + k*QWG_STEP quantises h block k
-        const int qk = (b - QWG0) / QWG_STEP;
-        const bool quantiser = wv == 1 && b >= QWG0 && (b - QWG0) % QWG_STEP == 0;
+        // down role: slot dslot (if below S), rows drow0 .. +63; wave wv takes
+        // rows drow0 + 16wv .. +15, 8 lanes per row (lane group dg, sub-task dq)
+        const int dslot = sb / DWG_PER_SLOT, drow0 = (sb % DWG_PER_SLOT) * DROWS;
+        const int dq = lane & 7, dg = lane >> 3;
 
         for (int l = 0; l < n_layer; l++) {
             const qmag_moe_layer &L = layers[l];
@@ -563,8 +553,10 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             const bool last = l + 1 == n_layer;
             TR(0);
 
-            // ---- all logits -> softmax, top-K (wave 0).  These workgroups
-            // wait here through the core's part of the layer: one word first.
+            // ---- all logits -> softmax, top-K (wave 0); meanwhile waves 1-3
+            // fetch the Q8_K(x_l) record, published with the logits.  These
+            // workgroups wait here through the core's part of the layer: one
+            // word first.
             bool ok = true;
             if (wv == 0) {
                 uint32_t g1[1];
@@ -578,11 +570,30 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 route_topk(lg, E, K, my_sel, my_w);
                 if (lane < K) s_sel[lane] = my_sel;
                 TR(6);
+            } else {
+                uint32_t g1[1];
+                ok = poll<1>(tg->xq[rep], [&](int) { return lane == 0 ? XR_G + (b & 7) : -1; }, seq, g1, abort_flag);
+                uint32_t v[2][2];
+                auto xp = [&](int k) {
+                    const int p = tid - 64 + 192 * k;  // word pair (the whole record is written)
+                    return p < XR_WORDS / 2 ? 4 * p + 3 : -1;
+                };
+                ok = ok && pollq<2>(rs, TW_XQ + rep * XR_WORDS, xp, seq, v, abort_flag);
+#pragma unroll
+                for (int k = 0; k < 2; k++)
+                    if (xp(k) >= 0) ((uint2 *)s_xrec)[xp(k) >> 2] = make_uint2(v[k][0], v[k][1]);
             }
             if (!wg_all(ok, s_vote, 1)) return;
             TR(2);
 
-            // ---- gate/up row pairs of this wave, then Q8_K(x_l)
+            // ---- gate/up row pairs of this wave, then (down role) its down
+            // rows, all requests issued back to back; the h computation waits
+            // only for the gate/up part.  The slab bases are read once,
+            // wave-uniform (scalar loads), then picked per lane: a per-lane
+            // read of the layer table would be a vector load whose wait also
+            // waits for the weight loads before it.
+            const uint8_t *const ge = (const uint8_t *)L.gate_exps, *const ue = (const uint8_t *)L.up_exps;
+            const uint8_t *const gsh = (const uint8_t *)L.gate_shexp, *const ush = (const uint8_t *)L.up_shexp;
             uint4 gh[MAX_RP], g0[MAX_RP], g1[MAX_RP];
 #pragma unroll
             for (int j = 0; j < MAX_RP; j++) {
@@ -590,27 +601,23 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 const int rp = gwv + j * GU_WAVES;
                 const int slot = rp / F;
                 if (rp < S * F) {
-                    const uint8_t *m = slot < K ? (const uint8_t *)(half ? L.up_exps : L.gate_exps) +
-                                                      (size_t)s_sel[slot] * GU_SLAB
-                                                : (const uint8_t *)(half ? L.up_shexp : L.gate_shexp);
+                    const uint8_t *m = slot < K ? (half ? ue : ge) + (size_t)s_sel[slot] * GU_SLAB : (half ? ush : gsh);
                     const uint8_t *blk = m + (size_t)(rp % F) * GU_ROW + (size_t)gib * Q4K_BYTES;
                     gh[j] = ld16(blk);
                     g0[j] = ld16(blk + 16 + 32 * gg);
                     g1[j] = ld16(blk + 32 + 32 * gg);
                 }
             }
-            {
-                uint32_t v[2][2];
-                auto xp = [&](int k) {
-                    const int p = tid + 256 * k;       // word pair (the whole record is written)
-                    return p < XR_WORDS / 2 ? 4 * p + 3 : -1;
-                };
-                ok = pollq<2>(rs, TW_XQ + rep * XR_WORDS, xp, seq, v, abort_flag);
+            // down role: this wave's down rows into registers (consumed after
+            // the h gather)
+            const bool down = dslot < S;              // workgroup-uniform
+            DRaw<TD> dr[DN_ROUNDS];
+            if (down) {
+                const uint8_t *slab = dslot < K ? (const uint8_t *)L.down_exps + (size_t)s_sel[dslot] * DN_SLAB
+                                                : (const uint8_t *)L.down_shexp;
 #pragma unroll
-                for (int k = 0; k < 2; k++)
-                    if (xp(k) >= 0) ((uint2 *)s_xrec)[xp(k) >> 2] = make_uint2(v[k][0], v[k][1]);
+                for (int j = 0; j < DN_ROUNDS; j++) d_load<TD>(dr[j], slab, drow0 + 16 * wv + 8 * j + dg, dq);
             }
-            if (!wg_all(ok, s_vote, 2)) return;
             TR(3);
 
             // ---- h = silu(g) * u for the wave's row pairs, one store for all
@@ -642,22 +649,36 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 }
             }
             if (lane < MAX_RP && gwv + lane * GU_WAVES < S * F)
-                st64(tg->h + gwv + lane * GU_WAVES, __float_as_uint(my_h), seq);
+                st64(rs, TW_H + gwv + lane * GU_WAVES, __float_as_uint(my_h), seq);
             TR(4);
 
-            // ---- quantiser: h block qk -> Q8_K(h) block record
-            if (quantiser && qk < S * NBF) {
-                uint32_t v[2][2];
-                ok = pollq<2>(rs, TW_H, [&](int k) { return 4 * (qk * (QK_K / 2) + 2 * lane + k) + 3; }, seq, v,
-                              abort_flag);
-                const float4 hv = make_float4(__uint_as_float(v[0][0]), __uint_as_float(v[0][1]),
-                                              __uint_as_float(v[1][0]), __uint_as_float(v[1][1]));
-                if (last) *(float4 *)(g_h + qk * QK_K + 4 * lane) = hv;      // stage copy
-                const Q8Lane q = q8k_quant_lane(hv);
-                unsigned long long *o = tg->hq;
-                st64(o + qk * 64 + lane, q.packed, seq);
-                if ((lane & 3) == 0) st64(o + HR_S + qk * 16 + (lane >> 2), (uint32_t)q.gsum, seq);
-                if (lane == 0) st64(o + HR_D + qk, __float_as_uint(q.d), seq);
+            if (down) {
+                // ---- h of slot dslot: 256 word pairs, one per thread
+                {
+                    uint32_t v[1][2];
+                    ok = pollq<1>(rs, TW_H + dslot * F, [&](int) { return 4 * tid + 3; }, seq, v, abort_flag);
+                    ((float2 *)s_hs)[tid] = make_float2(__uint_as_float(v[0][0]), __uint_as_float(v[0][1]));
+                }
+                if (!wg_all(ok, s_vote, 3)) return;
+                // ---- Q8_K(h): waves 0 and 1 quantise one block each
+                if (wv < NBF) {
+                    const Q8Lane q = q8k_quant_lane(s_hs[wv * 64 + lane]);
+                    ((uint32_t *)s_hq)[wv * 64 + lane] = q.packed;
+                    if ((lane & 3) == 0) ((int *)s_hq)[HS_S + wv * 16 + (lane >> 2)] = q.gsum;
+                    if (lane == 0) ((float *)s_hq)[HS_D + wv] = q.d;
+                }
+                if (last && drow0 == 0) ((float2 *)g_h)[dslot * (F / 2) + tid] = ((const float2 *)s_hs)[tid];
+                __syncthreads();
+                TR(5);
+                // ---- down dots of the wave's 16 rows; y published per row
+#pragma unroll
+                for (int j = 0; j < DN_ROUNDS; j++) {
+                    float v = d_dot<TD>(dr[j], (const uint32_t *)s_hq, (const float *)s_hq + HS_D,
+                                        (const int *)s_hq + HS_S, dq);
+                    v = group_sum<8>(v);
+                    if (dq == 0) st64(rs, TW_Y + dslot * N + drow0 + 16 * wv + 8 * j + dg, __float_as_uint(v), seq);
+                }
+                TR(1);
             }
             // LDS is rewritten next layer only after this barrier
             __syncthreads();
@@ -758,6 +779,8 @@ static int fused_prepare(const qmag_moe_layer *L, int n_layer, hipStream_t s)
             QMAG_HIP(hipMalloc(&g_trace, need));
             g_trace_bytes = need;
         }
+        // phases a workgroup does not pass through read back as 0
+        QMAG_HIP(hipMemsetAsync(g_trace, 0, need, s));
     } else if (g_trace) {
         QMAG_HIP(hipStreamSynchronize(s));
         QMAG_HIP(hipFree(g_trace));
