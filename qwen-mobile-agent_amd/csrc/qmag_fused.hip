@@ -8,18 +8,22 @@
 //
 //   core workgroups 0..127 (16 per XCD) each own 16 rows of the hidden state.
 //     They compute the router logits (2 per workgroup, router rows staged in
-//     LDS one layer ahead), Q8_K(x) (workgroups 0..7, one 256-block each,
-//     with that block's share of the shared-expert gate input) and the
-//     combine + residual of their rows from the 9 slots' down outputs.
-//   stream workgroups 128..511 (1536 waves) compute the gate/up row pairs:
-//     slot s < n_used is routed expert sel[s], slot n_used the shared one,
-//     three row pairs per wave.  Then 32 of them per slot (288 for 9 slots)
-//     run that slot's down projection over 64 rows each: gather the slot's
-//     h, quantise it (Q8_K(h), two blocks, in LDS) and take the dots of
-//     their down rows, which were fetched into registers as soon as the
-//     selection was known.  Spreading the down dots over 288 workgroups,
-//     each needing one slot's h, keeps both the gathers and the integer
-//     work per workgroup small.
+//     LDS one layer ahead), Q8_K(x) (workgroups 0..7 publish one 256-block
+//     each, with that block's share of the shared-expert gate input; every
+//     core workgroup also keeps its own copy) and the combine + residual of
+//     their rows from the 9 slots' down outputs.
+//   stream workgroups 128..511 run the softmax/top-k themselves.
+//   Every wave (2048) takes up to two routed gate/up row pairs (slot s <
+//   n_used is expert sel[s]), so each CU carries the same share whichever
+//   two workgroups it holds.  The shared expert's 512 row pairs go to waves
+//   2, 3 of workgroups 256..511, idle during the top-k: their rows are
+//   fetched at layer start and h published as soon as Q8_K(x) is in.
+//   Down projection: 32 units of 64 rows per slot.  A unit gathers its slot's
+//   h, quantises it (Q8_K(h), two blocks, in LDS) and takes the dots of its
+//   down rows, held in registers; routed units sit in workgroups 256..511
+//   (one per CU), the shared slot's in 128..159 (its h is out early).
+//   Spreading the down dots over 288 workgroups, each needing one slot's h,
+//   keeps both the gathers and the integer work per workgroup small.
 //
 // Hand-offs of one layer (each a set of tagged words, see below):
 //   x_l rows      core -> core            (2048 words, read by 128 workgroups)
@@ -60,12 +64,20 @@ constexpr int CORE = 128;                         // core workgroups
 constexpr int CROWS = N / CORE;                   // 16 hidden rows per core workgroup
 constexpr int WROWS = CROWS / 4;                  // 4 per core wave
 constexpr int NLOG = 256 / CORE;                  // 2 router logits per core workgroup
-constexpr int GU_WAVES = (WGS - CORE) * 4;        // 1536 gate/up waves
-constexpr int MAX_RP = (SMAX * F + GU_WAVES - 1) / GU_WAVES;   // 3 row pairs per wave
-constexpr int DROWS = 64;                         // down rows per down workgroup (one slot)
+constexpr int GU_WAVES = WGS * 4;                 // every wave takes routed gate/up row pairs
+constexpr int MAX_RP = (8 * F + GU_WAVES - 1) / GU_WAVES;      // 2 routed row pairs per wave
+// the shared expert's row pair i: workgroup SH_WG0 + i/2, wave 2 + i%2 (the
+// second workgroup of every CU when workgroups fill the CUs in order)
+constexpr int SH_WG0 = WGS / 2;
+static_assert(F <= 2 * (WGS - SH_WG0), "shared row pairs out of range");
+constexpr int DROWS = 64;                         // down rows per down unit (one slot)
 constexpr int DWG_PER_SLOT = N / DROWS;           // 32
 constexpr int DN_ROUNDS = DROWS / 4 / 8;          // 16 rows per wave, 8 lanes per row: 2 rounds
-static_assert(CORE + SMAX * DWG_PER_SLOT <= WGS, "down workgroups out of range");
+// routed down unit u (slot u/32) in workgroup RDN_WG0 + u, one per CU;
+// shared-slot unit r in workgroup SDN_WG0 + r (its h is out early)
+constexpr int RDN_WG0 = WGS / 2, SDN_WG0 = CORE;
+static_assert(RDN_WG0 + 8 * DWG_PER_SLOT <= WGS && SDN_WG0 + DWG_PER_SLOT <= RDN_WG0,
+              "down workgroups out of range");
 constexpr long SPIN_LIMIT = 1L << 22;
 
 // Q8_K records are laid out exactly as the LDS copy their readers keep, so a
@@ -340,7 +352,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
 {
     __shared__ float4 s_x[N / 4];                 // core: x_l
     __shared__ float4 s_wr[NLOG][N / 4];          // core: this workgroup's router rows
-    __shared__ uint4 s_xrec[(XR_WORDS + 3) / 4];  // stream: the Q8_K(x_l) record
+    __shared__ uint4 s_xrec[(XR_WORDS + 3) / 4];  // the Q8_K(x_l) record
     __shared__ float4 s_hs[F / 4];                // down: h of the slot
     __shared__ uint4 s_hq[(HS_WORDS + 3) / 4];    // down: Q8_K of that h
     __shared__ float s_gsp[NBE];                  // core: shared-gate input partials
@@ -353,6 +365,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
     const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), tid = (int)threadIdx.x;
     const int b = (int)blockIdx.x;
     const int rep = b % REP;
+    const bool core = b < CORE;
     const Rsrc rs = __builtin_amdgcn_make_buffer_rsrc(tg, 0, (int)sizeof(Tagged), 0x00020000);
     // the 256 logits of replica rep, lane's pairs l and l + 64 (experts
     // l + 64j, j = 0..3); a half is needed only for an expert below E
@@ -375,34 +388,109 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
     constexpr size_t GU_SLAB = (size_t)F * GU_ROW;                     // 589,824
     constexpr size_t DN_SLAB = (size_t)N * NBF * (TD == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES);
 
+    // ---- roles shared by both kinds of workgroup
+    // routed gate/up row pairs: global wave gw takes rows gw + j*GU_WAVES
+    const int gw = b * 4 + wv;
+    const int half = lane >> 5, l32 = lane & 31;
+    const int gib = l32 >> 2, gg = l32 & 3;       // gate/up task: block, 64-lane group
+    // shared-expert row pair (at most one per wave): waves 2, 3 of the
+    // workgroups from SH_WG0 on, which are idle while wave 0 runs the top-k
+    const int sh_row = b >= SH_WG0 && wv >= 2 ? 2 * (b - SH_WG0) + (wv - 2) : F;
+    // down role: a routed unit (slot u/32, rows (u%32)*64 ..) in workgroup
+    // RDN_WG0 + u, a shared-slot unit in workgroup SDN_WG0 + r; wave wv takes
+    // rows drow0 + 16wv .. +15, 8 lanes per row (lane group dg, sub-task dq)
+    const int dunit = b >= RDN_WG0 ? b - RDN_WG0 : -1;
+    const bool sh_down = b >= SDN_WG0 && b < SDN_WG0 + DWG_PER_SLOT;
+    const int drow0 = (dunit >= 0 ? dunit % DWG_PER_SLOT : b - SDN_WG0) * DROWS;
+    const int dq = lane & 7, dg = lane >> 3;
+
     // optional phase timestamps (100 MHz real-time counter), thread 0 only
 #define TR(i)                                                                              \
     if (trace && threadIdx.x == 0)                                                         \
         trace[((size_t)b * n_layer + l) * 8 + (i)] = __builtin_amdgcn_s_memrealtime();
 
-    if (b < CORE) {
-        // ================================================================ core
-        // rows r0 .. r0+15; wave wv owns r0+4wv .. +3, lane i < 4 keeps the
-        // residual value of row r0 + 4wv + i
-        const int r0 = b * CROWS;
-        // the router rows of layer l go straight into LDS one layer ahead
-        // (layer 0's here, layer l+1's once layer l's logits are computed)
-        auto load_router_rows = [&](const qmag_moe_layer &Ln) {
+    // core: rows r0 .. r0+15; wave wv owns r0+4wv .. +3, lane i < 4 keeps the
+    // residual value of row r0 + 4wv + i
+    const int r0 = b * CROWS;
+    // core: the router rows of layer l go straight into LDS, issued by wave
+    // 3 alone right after it published x_l (layer 0's before the loop): the
+    // HBM is idle then, and waves 0-2, which poll x_l, keep no loads in
+    // flight ahead of their polls
+    auto load_router_rows = [&](const qmag_moe_layer &Ln) {
 #pragma unroll
-            for (int j = 0; j < NLOG; j++) {
-                const int e = NLOG * b + j;
-                if (e < Ln.n_expert) {
-                    const float4 *row = (const float4 *)(Ln.gate_inp + (size_t)e * N);
+        for (int j = 0; j < NLOG; j++) {
+            const int e = NLOG * b + j;
+            if (e < Ln.n_expert) {
+                const float4 *row = (const float4 *)(Ln.gate_inp + (size_t)e * N);
 #pragma unroll
-                    for (int k = 0; k < 2; k++)
-                        __builtin_amdgcn_global_load_lds((const void *)(row + tid + 256 * k),
-                                                         (__attribute__((address_space(3))) void *)&s_wr[j][64 * wv + 256 * k],
-                                                         16, 0, 0);
-                }
+                for (int k = 0; k < N / 4 / 64; k++)
+                    __builtin_amdgcn_global_load_lds((const void *)(row + lane + 64 * k),
+                                                     (__attribute__((address_space(3))) void *)&s_wr[j][64 * k],
+                                                     16, 0, 0);
             }
-        };
+        }
+    };
+    // gate/up helpers: the wave's Q8_K(x_l) operand from the record in LDS,
+    // one row pair's raw blocks, and h = silu(gate) * up of a row pair (lanes
+    // 0-31 hold the gate dot, 32-63 the up dot)
+    constexpr size_t GU_ROW_ = GU_ROW;
+    auto gu_load = [&](uint4 &rh, uint4 &q0, uint4 &q1, const uint8_t *slab, int row) {
+        const uint8_t *blk = slab + (size_t)row * GU_ROW_ + (size_t)gib * Q4K_BYTES;
+        rh = ld16(blk);
+        q0 = ld16(blk + 16 + 32 * gg);
+        q1 = ld16(blk + 32 + 32 * gg);
+    };
+    auto load_act = [&](Q4Act &a) {
+        const uint4 *xw = s_xrec + (gib * QK_K + 64 * gg) / 16;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint4 w = xw[k];
+            a.x[4 * k + 0] = w.x;
+            a.x[4 * k + 1] = w.y;
+            a.x[4 * k + 2] = w.z;
+            a.x[4 * k + 3] = w.w;
+        }
+        a.xd = ((const float *)s_xrec)[XR_D + gib];
+        const int *sp = (const int *)s_xrec + XR_S + gib * 16 + 4 * gg;
+        a.sx0 = (float)(sp[0] + sp[1]);
+        a.sx1 = (float)(sp[2] + sp[3]);
+    };
+    auto swiglu = [&](const Q4Act &a, const uint4 &rh, const uint4 &q0, const uint4 &q1) {
+        float v = q4_task(rh, q0, q1, a, gg);
+        v = group_sum<32>(v);
+        auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        const float u = __uint_as_float(pr[1]);
+        return (v / (1.0f + expf(-v))) * u;
+    };
+    // the routed experts' gate/up row pairs of this wave: requested, then
+    // computed and published (one store for all)
+    auto routed_gate_up = [&](const qmag_moe_layer &L, int K, uint32_t seq) {
+        const uint8_t *const ge = (const uint8_t *)L.gate_exps, *const ue = (const uint8_t *)L.up_exps;
+        uint4 gh[MAX_RP], g0[MAX_RP], g1[MAX_RP];
+#pragma unroll
+        for (int j = 0; j < MAX_RP; j++) {
+            gh[j] = g0[j] = g1[j] = make_uint4(0, 0, 0, 0);
+            const int rp = gw + j * GU_WAVES, slot = rp / F;
+            if (rp < K * F) gu_load(gh[j], g0[j], g1[j], (half ? ue : ge) + (size_t)s_sel[slot] * GU_SLAB, rp % F);
+        }
+        Q4Act a;
+        load_act(a);
+        float my_h = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MAX_RP; j++) {
+            if (gw + j * GU_WAVES < K * F) {           // wave-uniform
+                const float hv = swiglu(a, gh[j], g0[j], g1[j]);
+                if (lane == j) my_h = hv;
+            }
+        }
+        if (lane < MAX_RP && gw + lane * GU_WAVES < K * F)
+            st64(rs, TW_H + gw + lane * GU_WAVES, __float_as_uint(my_h), seq);
+    };
+
+    if (core) {
+        // ================================================================ core
         float xres = lane < WROWS ? x[r0 + WROWS * wv + lane] : 0.0f;
-        load_router_rows(layers[0]);
+        if (wv == 3) load_router_rows(layers[0]);
 
         for (int l = 0; l < n_layer; l++) {
             const qmag_moe_layer &L = layers[l];
@@ -433,21 +521,31 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             if (!wg_all(ok, s_vote, 0)) return;
             TR(1);
 
-            // ---- logits (waves 0, 1, each published in every replica);
-            // Q8_K(x) block b and its shared-gate partial (wave 2, b < 8)
+            // ---- logits (waves 0, 1, each published in every replica), then
+            // this workgroup's own copy of the Q8_K(x_l) record (4 blocks
+            // each); Q8_K(x) block b and its shared-gate partial published
+            // (wave 2, b < 8); softmax/top-K (wave 3)
             if (wv < NLOG) {
                 const int e = NLOG * b + wv;
                 if (e < E) {
                     float s = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
-                        const float4 a = s_x[lane + 64 * j], w = s_wr[wv][lane + 64 * j];
-                        s += w.x * a.x + w.y * a.y + w.z * a.z + w.w * a.w;
+                        const float4 xa = s_x[lane + 64 * j], w = s_wr[wv][lane + 64 * j];
+                        s += w.x * xa.x + w.y * xa.y + w.z * xa.z + w.w * xa.w;
                     }
                     s = group_sum<64>(s);
                     if (L.router_bias) s += ldg(L.router_bias + e);
                     if (lane < REP) st64(rs, TW_LOGITS + lane * 256 + logit_pos(e), __float_as_uint(s), seq);
                     if (last && lane == 0) g_logits[e] = s;
+                }
+#pragma unroll
+                for (int k = 0; k < NBE / 2; k++) {
+                    const int blk = wv * (NBE / 2) + k;
+                    const Q8Lane q = q8k_quant_lane(s_x[blk * 64 + lane]);
+                    ((uint32_t *)s_xrec)[blk * 64 + lane] = q.packed;
+                    if ((lane & 3) == 0) ((int *)s_xrec)[XR_S + blk * 16 + (lane >> 2)] = q.gsum;
+                    if (lane == 0) ((float *)s_xrec)[XR_D + blk] = q.d;
                 }
             } else if (wv == 2 && b < NBE) {
                 const Q8Lane q = q8k_quant_lane(s_x[b * 64 + lane]);
@@ -465,8 +563,6 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                     if (lane == 1) st64(rs, o + XR_G + b, __float_as_uint(g), seq);
                 }
             } else if (wv == 3) {
-                // ---- all logits -> softmax, top-K (wave 3 has stored nothing
-                // since last layer's x rows)
                 float lg[4];
                 ok = read_logits(E, seq, lg);
                 int my_sel = 0;
@@ -484,9 +580,8 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             if (!wg_all(ok, s_vote, 1)) return;
             TR(2);
 
-            // ---- the next layer's router rows (this layer's are consumed)
-            if (!last) load_router_rows(layers[l + 1]);
-            TR(3);
+            routed_gate_up(L, K, seq);
+            TR(4);
 
             // ---- the down outputs of this workgroup's rows, every slot
             // (thread t < 8S: slot t/8, rows r0 + 2(t%8) + {0,1}), and the 8
@@ -508,7 +603,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 }
             }
             if (!wg_all(ok, s_vote, 2)) return;
-            TR(4);
+            TR(5);
 
             // ---- combine in the reference order (nn.c:614-629)
             if (lane < WROWS) {
@@ -534,18 +629,11 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 if (!last) st64(rs, TW_X + r0 + lane, __float_as_uint(s_xout[lane]), seq + 1u);
                 else x[r0 + lane] = s_xout[lane];
             }
+            if (!last && wv == 3) load_router_rows(layers[l + 1]);    // this layer's rows are consumed
             TR(6);
         }
     } else {
         // ============================================================== stream
-        const int sb = b - CORE, gwv = sb * 4 + wv;
-        const int half = lane >> 5, l32 = lane & 31;
-        const int gib = l32 >> 2, gg = l32 & 3;       // gate/up task: block, 64-lane group
-        // down role: slot dslot (if below S), rows drow0 .. +63; wave wv takes
-        // rows drow0 + 16wv .. +15, 8 lanes per row (lane group dg, sub-task dq)
-        const int dslot = sb / DWG_PER_SLOT, drow0 = (sb % DWG_PER_SLOT) * DROWS;
-        const int dq = lane & 7, dg = lane >> 3;
-
         for (int l = 0; l < n_layer; l++) {
             const qmag_moe_layer &L = layers[l];
             const int E = L.n_expert, K = L.n_used, S = K + 1;
@@ -553,11 +641,27 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             const bool last = l + 1 == n_layer;
             TR(0);
 
-            // ---- all logits -> softmax, top-K (wave 0); meanwhile waves 1-3
-            // fetch the Q8_K(x_l) record, published with the logits.  These
-            // workgroups wait here through the core's part of the layer: one
-            // word first.
+            // ---- rows that do not depend on the selection, requested at
+            // layer start while the HBM is otherwise idle: the shared
+            // expert's gate/up row pair of this wave and, in the shared slot's
+            // down workgroups, their down rows
+            uint4 sh_h = make_uint4(0, 0, 0, 0), sh_0 = sh_h, sh_1 = sh_h;
+            if (sh_row < F) gu_load(sh_h, sh_0, sh_1, (const uint8_t *)(half ? L.up_shexp : L.gate_shexp), sh_row);
+            const int dslot = dunit >= 0 ? dunit / DWG_PER_SLOT : sh_down ? K : S;   // S: no down role
+            const bool down = dslot < S && (dunit < 0 || dslot < K);
+            DRaw<TD> dr[DN_ROUNDS];
+            auto dn_load = [&](const uint8_t *slab) {
+#pragma unroll
+                for (int j = 0; j < DN_ROUNDS; j++) d_load<TD>(dr[j], slab, drow0 + 16 * wv + 8 * j + dg, dq);
+            };
+            if (sh_down) dn_load((const uint8_t *)L.down_shexp);
+
             bool ok = true;
+            // ---- softmax/top-K (wave 0); meanwhile waves 2, 3 each fetch the
+            // whole Q8_K(x_l) record, published with the logits, and the
+            // shared-expert row pair among them is computed and published at
+            // once.  These workgroups wait here through the core's part of the
+            // layer: one word first.
             if (wv == 0) {
                 uint32_t g1[1];
                 ok = poll<1>(tg->logits[rep], [&](int) { return lane == 0 ? logit_pos((b * 37) % E) : -1; }, seq, g1,
@@ -570,89 +674,41 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 route_topk(lg, E, K, my_sel, my_w);
                 if (lane < K) s_sel[lane] = my_sel;
                 TR(6);
-            } else {
+            } else if (wv >= 2) {
                 uint32_t g1[1];
                 ok = poll<1>(tg->xq[rep], [&](int) { return lane == 0 ? XR_G + (b & 7) : -1; }, seq, g1, abort_flag);
-                uint32_t v[2][2];
+                constexpr int XP = (XR_WORDS / 2 + 63) / 64;   // 6 word pairs per lane
+                uint32_t v[XP][2];
                 auto xp = [&](int k) {
-                    const int p = tid - 64 + 192 * k;  // word pair (the whole record is written)
+                    const int p = lane + 64 * k;       // word pair (the whole record is written)
                     return p < XR_WORDS / 2 ? 4 * p + 3 : -1;
                 };
-                ok = ok && pollq<2>(rs, TW_XQ + rep * XR_WORDS, xp, seq, v, abort_flag);
+                ok = ok && pollq<XP>(rs, TW_XQ + rep * XR_WORDS, xp, seq, v, abort_flag);
 #pragma unroll
-                for (int k = 0; k < 2; k++)
+                for (int k = 0; k < XP; k++)
                     if (xp(k) >= 0) ((uint2 *)s_xrec)[xp(k) >> 2] = make_uint2(v[k][0], v[k][1]);
+                if (sh_row < F) {
+                    Q4Act a;
+                    load_act(a);
+                    const float hv = swiglu(a, sh_h, sh_0, sh_1);
+                    if (lane == 0) st64(rs, TW_H + K * F + sh_row, __float_as_uint(hv), seq);
+                }
             }
             if (!wg_all(ok, s_vote, 1)) return;
             TR(2);
+            // the shared registers count as read on every path from here on,
+            // so no later write into them has to wait for the load queue
+            __asm__ volatile("" ::"v"(sh_h.x), "v"(sh_0.x), "v"(sh_1.x));
 
-            // ---- gate/up row pairs of this wave, then (down role) its down
-            // rows, all requests issued back to back; the h computation waits
-            // only for the gate/up part.  The slab bases are read once,
-            // wave-uniform (scalar loads), then picked per lane: a per-lane
-            // read of the layer table would be a vector load whose wait also
-            // waits for the weight loads before it.
-            const uint8_t *const ge = (const uint8_t *)L.gate_exps, *const ue = (const uint8_t *)L.up_exps;
-            const uint8_t *const gsh = (const uint8_t *)L.gate_shexp, *const ush = (const uint8_t *)L.up_shexp;
-            uint4 gh[MAX_RP], g0[MAX_RP], g1[MAX_RP];
-#pragma unroll
-            for (int j = 0; j < MAX_RP; j++) {
-                gh[j] = g0[j] = g1[j] = make_uint4(0, 0, 0, 0);
-                const int rp = gwv + j * GU_WAVES;
-                const int slot = rp / F;
-                if (rp < S * F) {
-                    const uint8_t *m = slot < K ? (half ? ue : ge) + (size_t)s_sel[slot] * GU_SLAB : (half ? ush : gsh);
-                    const uint8_t *blk = m + (size_t)(rp % F) * GU_ROW + (size_t)gib * Q4K_BYTES;
-                    gh[j] = ld16(blk);
-                    g0[j] = ld16(blk + 16 + 32 * gg);
-                    g1[j] = ld16(blk + 32 + 32 * gg);
-                }
-            }
-            // down role: this wave's down rows into registers (consumed after
-            // the h gather)
-            const bool down = dslot < S;              // workgroup-uniform
-            DRaw<TD> dr[DN_ROUNDS];
-            if (down) {
-                const uint8_t *slab = dslot < K ? (const uint8_t *)L.down_exps + (size_t)s_sel[dslot] * DN_SLAB
-                                                : (const uint8_t *)L.down_shexp;
-#pragma unroll
-                for (int j = 0; j < DN_ROUNDS; j++) d_load<TD>(dr[j], slab, drow0 + 16 * wv + 8 * j + dg, dq);
-            }
-            TR(3);
-
-            // ---- h = silu(g) * u for the wave's row pairs, one store for all
-            Q4Act a;
-            const uint4 *xw = s_xrec + (gib * QK_K + 64 * gg) / 16;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint4 w = xw[k];
-                a.x[4 * k + 0] = w.x;
-                a.x[4 * k + 1] = w.y;
-                a.x[4 * k + 2] = w.z;
-                a.x[4 * k + 3] = w.w;
-            }
-            a.xd = ((const float *)s_xrec)[XR_D + gib];
-            const int *sp = (const int *)s_xrec + XR_S + gib * 16 + 4 * gg;
-            a.sx0 = (float)(sp[0] + sp[1]);
-            a.sx1 = (float)(sp[2] + sp[3]);
-            float my_h = 0.0f;
-#pragma unroll
-            for (int j = 0; j < MAX_RP; j++) {
-                if (gwv + j * GU_WAVES < S * F) {          // wave-uniform
-                    float v = q4_task(gh[j], g0[j], g1[j], a, gg);
-                    v = group_sum<32>(v);
-                    auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
-                                                               false, false);
-                    const float u = __uint_as_float(pr[1]);
-                    const float hv = (v / (1.0f + expf(-v))) * u;
-                    if (lane == j) my_h = hv;
-                }
-            }
-            if (lane < MAX_RP && gwv + lane * GU_WAVES < S * F)
-                st64(rs, TW_H + gwv + lane * GU_WAVES, __float_as_uint(my_h), seq);
+            routed_gate_up(L, K, seq);
             TR(4);
 
             if (down) {
+                // ---- a routed slot's down rows, requested only now that the
+                // gate/up data is in: issued together with it they would share the
+                // HBM with the requests h is waiting for.  They land while the
+                // slot's h is gathered.
+                if (dslot < K) dn_load((const uint8_t *)L.down_exps + (size_t)s_sel[dslot] * DN_SLAB);
                 // ---- h of slot dslot: 256 word pairs, one per thread
                 {
                     uint32_t v[1][2];
@@ -680,6 +736,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 }
                 TR(1);
             }
+
             // LDS is rewritten next layer only after this barrier
             __syncthreads();
         }
