@@ -511,7 +511,15 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                     const int p = tid + 192 * k;         // word pair
                     return p < N / 2 ? 4 * p + 3 : -1;
                 };
-                ok = pollq<6>(rs, TW_X, xp, seq, v, abort_flag);
+                // one word of another workgroup's rows first: bulk polls
+                // from every core workgroup during the wait would load the
+                // memory system the other hand-offs share
+                {
+                    uint32_t g1[1];
+                    ok = poll<1>(tg->x, [&](int) { return lane == 0 ? ((b + CORE / 2) % CORE) * CROWS + CROWS - 1 : -1; },
+                                 seq, g1, abort_flag);
+                }
+                ok = ok && pollq<6>(rs, TW_X, xp, seq, v, abort_flag);
 #pragma unroll
                 for (int k = 0; k < 6; k++)
                     if (xp(k) >= 0)
@@ -712,6 +720,12 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 // ---- h of slot dslot: 256 word pairs, one per thread
                 {
                     uint32_t v[1][2];
+                    if (wv == 0) {                    // one word first, as for x
+                        uint32_t g1[1];
+                        ok = poll<1>(tg->h + dslot * F, [&](int) { return lane == 0 ? F - 1 - (b % 64) : -1; }, seq, g1,
+                                     abort_flag);
+                    }
+                    if (!wg_all(ok, s_vote, 0)) return;
                     ok = pollq<1>(rs, TW_H + dslot * F, [&](int) { return 4 * tid + 3; }, seq, v, abort_flag);
                     ((float2 *)s_hs)[tid] = make_float2(__uint_as_float(v[0][0]), __uint_as_float(v[0][1]));
                 }
