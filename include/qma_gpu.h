@@ -97,14 +97,14 @@ int qmag_prof_read(int kernel_id, long *count, double *total_ms);
 
 /* Options.  QMAG_OPT_FUSED (default 1): batch-1 MoE decode of the qwen35moe
    shape (n_embd 2048, n_ff 512, n_used <= 8, equal down types) runs as one
-   persistent cooperative kernel per token; 0 selects the per-stage launch
-   sequence (same results within the fp32 tolerance). */
+   persistent kernel launch per token through all layers; 0 selects the
+   per-stage launch sequence (same results within the fp32 tolerance). */
 #define QMAG_OPT_FUSED 1
 /* QMAG_OPT_TRACE (default 0): the fused decode kernel records, per
-   workgroup and layer, 8 phase timestamps of the 100 MHz device real-time
-   counter (layer start, after hop A, router done, after hop B, gate/up
-   start, gate/up done, after hop C, down done); qmag_trace_read copies the
-   last launch's [512][n_layer][8] uint64 array to the host. */
+   workgroup and layer, up to 8 phase timestamps of the 100 MHz device
+   real-time counter (slot 0 is the layer start; the other slots mark the
+   phases of the workgroup's role, 0 where it has none); qmag_trace_read
+   copies the last launch's [512][n_layer][8] uint64 array to the host. */
 #define QMAG_OPT_TRACE 2
 /* QMAG_OPT_COOP (default 0): 1 launches the fused decode kernel with
    hipLaunchCooperativeKernel (co-residency of its 512 workgroups guaranteed
