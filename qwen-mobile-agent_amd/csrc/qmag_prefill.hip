@@ -5,12 +5,13 @@
 //   topk_kernel          (qmag_moe.hip) softmax/top-k, Q8_K(x), shared gate
 //   group_kernel         (token, slot) pairs bucketed by expert; the shared
 //                        expert is bucket E with one pair per token
-//   gateup_grouped_kernel h = silu(x.G) * (x.U) per pair: 16 pairs x 16 rows
-//                        per wave, one v_mfma_i32_16x16x32_i8 per 32-wide
-//                        Q4_K sub-block with its 6-bit scale applied to the
-//                        int32 result, and one more against the sub-block's
-//                        min broadcast over its 32 k (the min term, summed in
-//                        the matrix core over the super-block)
+//   gateup_chunk_kernel  h = silu(x.G) * (x.U) per pair: chunks of up to 64
+//                        pairs of one expert x 64 gate and 64 up rows, one
+//                        v_mfma_i32_16x16x32_i8 per 16 pairs x 16 rows x
+//                        32-wide Q4_K sub-block with its 6-bit scale applied
+//                        to the int32 result, and one more against the
+//                        sub-block's min broadcast over its 32 k (the min
+//                        term, summed in the matrix core over the block)
 //   q8k_quant_kernel     Q8_K(h) per pair
 //   down_grouped_kernel  y[pair] = Q8_K(h) . D^T: Q6_K per 16-wide group (the
 //                        MFMA's other 16 k are zero) or Q4_K per sub-block
@@ -24,9 +25,10 @@
 // fp32 epilogue (scale * xd * integer sum) is associated differently from
 // the reference's per-sub-block fp32 terms, well inside 1e-4 of max|y|.
 //
-// Every expert's weights are read once per 16-pair block (the shared
-// expert's by every block of 16 tokens); the pair buffers (h: T*S*F fp32,
-// y: T*S*N fp32) stay in HBM between kernels.
+// Every expert's gate/up weights are read once per 64-pair chunk and its
+// down weights once per 16-pair block (the shared expert's by every chunk
+// or block of tokens); the pair buffers (h: T*S*F fp32, y: T*S*N fp32) stay
+// in HBM between kernels.
 #include "qmag_internal.h"
 
 namespace qmag {
@@ -86,15 +88,18 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
 
 // ---------------------------------------------------------------- group --
 // grp layout: cnt[E+1], off[E+2], tbo[E+2] (16-pair blocks per bucket,
-// prefix); blk[b] = the bucket of global 16-pair block b; perm[T*S] (pair
-// ids = t*S + slot, bucketed by expert).  Positions inside a bucket come
-// from LDS atomics; every pair's result is computed independently of its
-// neighbours, so the order does not change any output.
+// prefix), mco[E+2] (MC-pair chunks per bucket, prefix); blk[b] = the
+// bucket of global 16-pair block b, mblk[c] = the bucket of chunk c;
+// perm[T*S] (pair ids = t*S + slot, bucketed by expert).  Positions inside
+// a bucket come from LDS atomics; every pair's result is computed
+// independently of its neighbours, so the order does not change any output.
+constexpr int MC = 64;            // pairs per chunk of the chunked GEMMs (4 MFMA tiles)
+
 __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel, int T, int K, int E,
                                                      int *__restrict__ grp, int *__restrict__ blk,
-                                                     int *__restrict__ perm)
+                                                     int *__restrict__ mblk, int *__restrict__ perm)
 {
-    __shared__ int s_cnt[257], s_off[258], s_fill[257], s_inc[257], s_binc[257];
+    __shared__ int s_cnt[257], s_off[258], s_fill[257], s_inc[257], s_binc[257], s_minc[257];
     const int tid = (int)threadIdx.x, S = K + 1;
     for (int e = tid; e <= E; e += 1024) {
         s_cnt[e] = 0;
@@ -111,23 +116,26 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
     if (tid <= E) {
         s_inc[tid] = s_cnt[tid];
         s_binc[tid] = (s_cnt[tid] + PB - 1) / PB;
+        s_minc[tid] = (s_cnt[tid] + MC - 1) / MC;
     }
     __syncthreads();
     for (int d = 1; d <= 256; d <<= 1) {
-        int a = 0, b = 0;
+        int a = 0, b = 0, m = 0;
         if (tid <= E && tid >= d) {
             a = s_inc[tid - d];
             b = s_binc[tid - d];
+            m = s_minc[tid - d];
         }
         __syncthreads();
         if (tid <= E && tid >= d) {
             s_inc[tid] += a;
             s_binc[tid] += b;
+            s_minc[tid] += m;
         }
         __syncthreads();
     }
     if (tid <= E) {
-        int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
+        int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2), *mco = tbo + (E + 2);
         const int c = s_cnt[tid];
         s_off[tid] = s_inc[tid] - c;
         cnt[tid] = c;
@@ -135,9 +143,13 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
         const int nb = (c + PB - 1) / PB, b0 = s_binc[tid] - nb;
         tbo[tid] = b0;
         for (int i = 0; i < nb; i++) blk[b0 + i] = tid;
+        const int nm = (c + MC - 1) / MC, m0 = s_minc[tid] - nm;
+        mco[tid] = m0;
+        for (int i = 0; i < nm; i++) mblk[m0 + i] = tid;
         if (tid == E) {
             off[E + 1] = s_inc[E];
             tbo[E + 1] = s_binc[E];
+            mco[E + 1] = s_minc[E];
         }
     }
     __syncthreads();
@@ -321,59 +333,172 @@ __device__ __forceinline__ void stage_q8k(const int *s_pair, RowOf row_of, const
     }
 }
 
-// ---------------------------------------------------------- gate / up --
-// grid: (max 16-pair blocks) x (F / 32); a workgroup = one pair block x 32
-// row pairs: waves 0-1 the gate rows, waves 2-3 the up rows (one weight
-// matrix per wave keeps all its bytes in flight at once), met in LDS for
-// h[pair][row] = silu(g) * u.  The weight loads are issued before the
-// activations are staged.
+// ------------------------------------------- gate / up, chunked streaming --
+// grid: (max MC-pair chunks) x (F / GU_RC); a workgroup = one chunk of up to
+// 64 pairs of one bucket x 64 gate rows and the same 64 up rows: waves 0-1
+// take the gate rows, 2-3 the up rows, 32 rows (2 MFMA row tiles) each.
+// The K loop runs over the NBE super-blocks with both operands double
+// buffered: the next block's weight bytes (registers) and Q8_K(x) rows
+// (loaded to registers, written to the other LDS buffer after the MFMAs)
+// are requested before the current block's MFMAs, so every wave streams
+// weights continuously (a block ahead: 6 KB per wave in flight, four
+// workgroups per CU) and each activation row is staged once per 64 rows.
+constexpr int GU_RC = 64;
+constexpr int GU_RT = 2;          // MFMA row tiles per wave
+constexpr int ARB = QK_K + 16;    // LDS bytes per staged pair row of one block (16 B pad vs bank conflicts)
+
+struct GUW {                      // a lane's bytes of one super-block of its GU_RT rows
+    uint4 hdr[GU_RT];
+    uint2 qs[GU_RT][4];
+};
+
 template <int NBE>
-__global__ __launch_bounds__(256, 2) void gateup_grouped_kernel(
+__global__ __launch_bounds__(256, 2) void gateup_chunk_kernel(
     const uint8_t *__restrict__ gate_exps, const uint8_t *__restrict__ up_exps,
     const uint8_t *__restrict__ gate_sh, const uint8_t *__restrict__ up_sh, int E, int S, int F,
-    const int *__restrict__ grp, const int *__restrict__ blk, const int *__restrict__ perm,
-    const int8_t *__restrict__ xq, const float *__restrict__ xd, const int16_t *__restrict__ xs,
-    float *__restrict__ h)
+    const int *__restrict__ grp, const int *__restrict__ mblk, const int *__restrict__ perm,
+    const int8_t *__restrict__ xq, const float *__restrict__ xd, float *__restrict__ h)
 {
-    constexpr int CH = NBE < 8 ? NBE : 8;
-    __shared__ __align__(16) int8_t s_aq[PB * arow<NBE>()];
-    __shared__ __align__(16) float s_ad[NBE * PB];
-    __shared__ float s_res[2][32][PB + 1];
-    __shared__ int s_pair[PB];
-    const int rblocks = F / 32;
-    const int tbg = (int)blockIdx.x / rblocks, rb = (int)blockIdx.x % rblocks;
-    const int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
-    if (tbg >= tbo[E + 1]) return;
-    const int e = blk[tbg];
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), lr = lane & 15, q = lane >> 4;
-    const int mat = wv >> 1, lrow = 16 * (wv & 1) + lr;       // 0 gate / 1 up, row within the 32
-    const size_t rowb = (size_t)NBE * Q4K_BYTES;
-    const uint8_t *W = (mat == 0 ? (e < E ? gate_exps + (size_t)e * F * rowb : gate_sh)
-                                 : (e < E ? up_exps + (size_t)e * F * rowb : up_sh)) +
-                       (size_t)(rb * 32 + lrow) * rowb;
-    Q4W<CH> w;
-    q4w_load(w, W, 0);
-    const int ltb = tbg - tbo[e];
-    if (threadIdx.x < PB) {
-        const int i = PB * ltb + (int)threadIdx.x;
-        s_pair[threadIdx.x] = i < cnt[e] ? perm[off[e] + i] : -1;
-    }
+    __shared__ __align__(16) int8_t s_aq[2][MC * ARB];
+    __shared__ __align__(16) float s_ad[2][MC];
+    __shared__ int s_pair[MC];
+    const int rchunks = F / GU_RC;
+    const int u = (int)blockIdx.x / rchunks, rc = (int)blockIdx.x % rchunks;
+    const int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2), *mco = tbo + (E + 2);
+    if (u >= mco[E + 1]) return;
+    const int e = mblk[u], mc = u - mco[e];
+    const int npair = min(MC, cnt[e] - mc * MC), mtn = (npair + 15) / 16;
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), tid = (int)threadIdx.x;
+    const int lr = lane & 15, q = lane >> 4;
+    const int mat = wv >> 1, rbase = rc * GU_RC + 16 * GU_RT * (wv & 1);
+    constexpr size_t rowb = (size_t)NBE * Q4K_BYTES;
+    const uint8_t *W = mat == 0 ? (e < E ? gate_exps + (size_t)e * F * rowb : gate_sh)
+                                : (e < E ? up_exps + (size_t)e * F * rowb : up_sh);
+    if (tid < MC) s_pair[tid] = tid < npair ? perm[off[e] + mc * MC + tid] : -1;
     __syncthreads();
-    stage_q8k<NBE>(s_pair, [&](int pr) { return pr / S; }, xq, xd, s_aq, s_ad);
-    __syncthreads();
-    float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    q4w_mma<NBE, CH>(w, 0, s_aq, s_ad, r);
-    for (int c0 = CH; c0 < NBE; c0 += CH) {
-        q4w_load(w, W, c0);
-        q4w_mma<NBE, CH>(w, c0, s_aq, s_ad, r);
-    }
+
+    auto w_load = [&](GUW &w, int kb) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) s_res[mat][lrow][4 * q + i] = r[i];
+        for (int rt = 0; rt < GU_RT; rt++) {
+            const uint8_t *blk = W + (size_t)(rbase + 16 * rt + lr) * rowb + (size_t)kb * Q4K_BYTES;
+            w.hdr[rt] = ld16(blk);
+#pragma unroll
+            for (int g = 0; g < 4; g++) w.qs[rt][g] = ld8(blk + 16 + 32 * g + 8 * q);
+        }
+    };
+    // one block of the chunk's Q8_K(x) rows: 64 rows x 16 parts of 16 bytes,
+    // 4 per thread, plus the 64 scales
+    uint4 sv[4];
+    float sd = 0.0f;
+    auto s_load = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = tid + 256 * i, p = c >> 4, part = c & 15, pr = s_pair[p];
+            sv[i] = pr >= 0 ? *(const uint4 *)(xq + (size_t)(pr / S) * (NBE * QK_K) + kb * QK_K + part * 16)
+                            : make_uint4(0, 0, 0, 0);
+        }
+        if (tid < MC) sd = s_pair[tid] >= 0 ? xd[(size_t)(s_pair[tid] / S) * NBE + kb] : 0.0f;
+    };
+    auto s_store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = tid + 256 * i, p = c >> 4, part = c & 15;
+            *(uint4 *)(&s_aq[buf][p * ARB + part * 16]) = sv[i];
+        }
+        if (tid < MC) s_ad[buf][tid] = sd;
+    };
+    float r[GU_RT][4][4];
+#pragma unroll
+    for (int rt = 0; rt < GU_RT; rt++)
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) r[rt][mt][i] = 0.0f;
+    auto compute = [&](const GUW &w, int buf) {
+        const int8_t *aq = s_aq[buf];
+#pragma unroll
+        for (int rt = 0; rt < GU_RT; rt++) {
+            // the 8 six-bit scales and mins of the row's block (src/q8k.c:22-30)
+            const uint32_t y = w.hdr[rt].y, z = w.hdr[rt].z, x4 = w.hdr[rt].w;
+            const uint32_t sc_lo = y & 0x3F3F3F3Fu, m_lo = z & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (x4 & 0x0F0F0F0Fu) | (((y >> 6) & 0x03030303u) << 4);
+            const uint32_t m_hi = ((x4 >> 4) & 0x0F0F0F0Fu) | (((z >> 6) & 0x03030303u) << 4);
+            const float d = h2f(w.hdr[rt].x & 0xffff), dmin = h2f(w.hdr[rt].x >> 16);
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
+                if (mt < mtn) {                  // workgroup-uniform
+                    int acc[4] = {0, 0, 0, 0};
+                    v4i accm = {0, 0, 0, 0};
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const long a = *(const long *)(aq + (16 * mt + lr) * ARB + 32 * j + 8 * q);
+                        const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, pack_nib(w.qs[rt][j >> 1], j & 1),
+                                                                            v4i{0, 0, 0, 0}, 0, 0, 0);
+                        const int sc = (int)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 63);
+                        const uint32_t mb = (((j < 4 ? m_lo : m_hi) >> (8 * (j & 3))) & 63) * 0x01010101u;
+                        accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, (long)(((unsigned long long)mb << 32) | mb),
+                                                                     accm, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[i] += sc * p[i];
+                    }
+                    const float4 xs = *(const float4 *)(s_ad[buf] + 16 * mt + 4 * q);
+                    r[rt][mt][0] += (d * xs.x) * (float)acc[0] - (dmin * xs.x) * (float)accm[0];
+                    r[rt][mt][1] += (d * xs.y) * (float)acc[1] - (dmin * xs.y) * (float)accm[1];
+                    r[rt][mt][2] += (d * xs.z) * (float)acc[2] - (dmin * xs.z) * (float)accm[2];
+                    r[rt][mt][3] += (d * xs.w) * (float)acc[3] - (dmin * xs.w) * (float)accm[3];
+                }
+            }
+        }
+    };
+
+    GUW wa, wb;
+    w_load(wa, 0);
+    s_load(0);
+    s_store(0);
     __syncthreads();
-    for (int c = (int)threadIdx.x; c < 32 * PB; c += 256) {
-        const int row = c / PB, p = c % PB, pr = s_pair[p];
-        const float g = s_res[0][row][p], u = s_res[1][row][p];
-        if (pr >= 0) h[(size_t)pr * F + rb * 32 + row] = (g / (1.0f + expf(-g))) * u;
+    for (int kb = 0; kb < NBE; kb += 2) {
+        // block kb from (wa, buffer 0) while block kb+1 streams into (wb, buffer 1)
+        if (kb + 1 < NBE) {
+            w_load(wb, kb + 1);
+            s_load(kb + 1);
+        }
+        compute(wa, 0);
+        if (kb + 1 < NBE) s_store(1);
+        __syncthreads();
+        if (kb + 1 < NBE) {
+            if (kb + 2 < NBE) {
+                w_load(wa, kb + 2);
+                s_load(kb + 2);
+            }
+            compute(wb, 1);
+            if (kb + 2 < NBE) s_store(0);
+            __syncthreads();
+        }
+    }
+    // h = silu(g) * u: the up waves hand their results to the gate waves
+    // through LDS (the activation buffers are free now)
+    float *ex = (float *)&s_aq[0][0];
+    auto exi = [&](int rt, int mt, int i) { return ((((wv & 1) * GU_RT + rt) * 4 + mt) * 4 + i) * 64 + lane; };
+    if (mat == 1) {
+#pragma unroll
+        for (int rt = 0; rt < GU_RT; rt++)
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) ex[exi(rt, mt, i)] = r[rt][mt][i];
+    }
+    __syncthreads();
+    if (mat == 0) {
+#pragma unroll
+        for (int rt = 0; rt < GU_RT; rt++)
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int pr = s_pair[16 * mt + 4 * q + i];
+                    const float g = r[rt][mt][i], uu = ex[exi(rt, mt, i)];
+                    if (mt < mtn && pr >= 0) h[(size_t)pr * F + rbase + 16 * rt + lr] = (g / (1.0f + expf(-g))) * uu;
+                }
     }
 }
 
@@ -462,12 +587,12 @@ int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *lo
 }
 
 template <int NBE>
-static void launch_gu(const qmag_moe_layer *L, int S, int max_blocks, const int *grp, const int *blk,
-                      const int *perm, const int8_t *xq, const float *xd, const int16_t *xs, float *h, hipStream_t s)
+static void launch_gu(const qmag_moe_layer *L, int S, int max_chunks, const int *grp, const int *mblk,
+                      const int *perm, const int8_t *xq, const float *xd, float *h, hipStream_t s)
 {
-    hipLaunchKernelGGL(gateup_grouped_kernel<NBE>, dim3(max_blocks * (L->n_ff / 32)), dim3(256), 0, s,
+    hipLaunchKernelGGL(gateup_chunk_kernel<NBE>, dim3(max_chunks * (L->n_ff / GU_RC)), dim3(256), 0, s,
                        (const uint8_t *)L->gate_exps, (const uint8_t *)L->up_exps, (const uint8_t *)L->gate_shexp,
-                       (const uint8_t *)L->up_shexp, L->n_expert, S, L->n_ff, grp, blk, perm, xq, xd, xs, h);
+                       (const uint8_t *)L->up_shexp, L->n_expert, S, L->n_ff, grp, mblk, perm, xq, xd, h);
 }
 
 template <int NBF>
@@ -485,24 +610,27 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
 {
     const int N = L->n_embd, F = L->n_ff, E = L->n_expert, K = L->n_used, S = K + 1;
     int st;
-    // an upper bound of the 16-pair blocks: sum ceil(n_e / 16) <= T*K/16 + E, plus the shared bucket
+    // upper bounds of the 16-pair blocks and the MC-pair chunks: sum
+    // ceil(n_e / 16) <= T*K/16 + E, plus the shared bucket
     const int max_blocks = (T * K + PB - 1) / PB + E + (T + PB - 1) / PB;
-    int *grp = (int *)workspace(WS_GRP, sizeof(int) * ((size_t)3 * (E + 2) + max_blocks + (size_t)T * S), &st);
+    const int max_chunks = (T * K + MC - 1) / MC + E + (T + MC - 1) / MC;
+    int *grp = (int *)workspace(WS_GRP, sizeof(int) * ((size_t)4 * (E + 2) + max_blocks + max_chunks + (size_t)T * S),
+                                &st);
     if (st) return st;
-    int *blk = grp + 3 * (E + 2), *perm = blk + max_blocks;
+    int *blk = grp + 4 * (E + 2), *mblk = blk + max_blocks, *perm = mblk + max_chunks;
     float *y = (float *)workspace(WS_Y, sizeof(float) * (size_t)T * S * N, &st);
     if (st) return st;
 
     prof_begin(PROF_GROUP, s);
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, sel, T, K, E, grp, blk, perm);
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, sel, T, K, E, grp, blk, mblk, perm);
     prof_end(PROF_GROUP, s);
     prof_begin(PROF_GATEUP, s);
     switch (N / QK_K) {
-    case 1: launch_gu<1>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
-    case 2: launch_gu<2>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
-    case 4: launch_gu<4>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
-    case 8: launch_gu<8>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
-    default: launch_gu<16>(L, S, max_blocks, grp, blk, perm, xq, xd, xs, h, s); break;
+    case 1: launch_gu<1>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
+    case 2: launch_gu<2>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
+    case 4: launch_gu<4>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
+    case 8: launch_gu<8>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
+    default: launch_gu<16>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
     }
     prof_end(PROF_GATEUP, s);
     prof_begin(PROF_HQUANT, s);
