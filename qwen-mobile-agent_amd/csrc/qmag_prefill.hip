@@ -21,7 +21,10 @@
 //
 // Integer parity: each MFMA result is the exact int32 dot of one sub-block
 // (Q4_K) or group (Q6_K) -- the integer sums of src/q8k.c -- and the scale
-// products are accumulated exactly in int32 per super-block; only the
+// products are accumulated exactly in int32 per super-block (with 24-bit
+// multiplies, exact here: |MFMA result| <= 32*15*128 < 2^17 and the
+// scales are 6- or 8-bit; v_mad_i32_i24 runs at the full VALU rate where a
+// 32-bit multiply takes four passes); only the
 // fp32 epilogue (scale * xd * integer sum) is associated differently from
 // the reference's per-sub-block fp32 terms, well inside 1e-4 of max|y|.
 //
@@ -88,22 +91,34 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
 
 // ---------------------------------------------------------------- group --
 // grp layout: cnt[E+1], off[E+2], tbo[E+2] (16-pair blocks per bucket,
-// prefix), mco[E+2] (MC-pair chunks per bucket, prefix); blk[b] = the
-// bucket of global 16-pair block b, mblk[c] = the bucket of chunk c;
-// perm[T*S] (pair ids = t*S + slot, bucketed by expert).  Positions inside
-// a bucket come from LDS atomics; every pair's result is computed
+// prefix); blk[b] = the bucket of global 16-pair block b; chunk[c] = {bucket
+// (-1 past the last chunk), pairs, offset of its first pair in perm, 0}, one
+// int4 per MC-pair chunk, so a workgroup learns all it needs from one load;
+// perm[T*S] (pair ids = t*S + slot, bucketed by expert).  Positions
+// inside a bucket come from LDS atomics; every pair's result is computed
 // independently of its neighbours, so the order does not change any output.
+//
+// Chunk order (the dispatch order of the chunked GEMMs): every full chunk
+// first, then the partial ones by decreasing size, so the longest
+// workgroups start first and the grid ends on the shortest ones.
 constexpr int MC = 64;            // pairs per chunk of the chunked GEMMs (4 MFMA tiles)
 
 __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel, int T, int K, int E,
                                                      int *__restrict__ grp, int *__restrict__ blk,
-                                                     int *__restrict__ mblk, int *__restrict__ perm)
+                                                     int4 *__restrict__ chunk, int max_chunks,
+                                                     int *__restrict__ perm)
 {
-    __shared__ int s_cnt[257], s_off[258], s_fill[257], s_inc[257], s_binc[257], s_minc[257];
+    __shared__ int s_cnt[257], s_off[258], s_fill[257], s_inc[257], s_binc[257], s_finc[257];
+    __shared__ int s_bin[MC], s_binf[MC];     // partial chunks by MC - size
+    __shared__ int s_nch;
     const int tid = (int)threadIdx.x, S = K + 1;
     for (int e = tid; e <= E; e += 1024) {
         s_cnt[e] = 0;
         s_fill[e] = 0;
+    }
+    if (tid < MC) {
+        s_bin[tid] = 0;
+        s_binf[tid] = 0;
     }
     __syncthreads();
     // ids come from the top-k (always < E); clamp anyway, this indexes LDS
@@ -111,12 +126,15 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
     for (int p = tid; p < T * K; p += 1024) atomicAdd(&s_cnt[expert(p)], 1);
     if (tid == 0) s_cnt[E] = T;      // shared expert: every token
     __syncthreads();
-    // inclusive prefix sums of the pair counts and of the 16-pair block
-    // counts over the E + 1 buckets (Hillis-Steele in LDS, 9 steps)
+    // inclusive prefix sums of the pair counts, the 16-pair block counts and
+    // the full-chunk counts over the E + 1 buckets (Hillis-Steele in LDS, 9
+    // steps); the partial chunks are counted per size
     if (tid <= E) {
-        s_inc[tid] = s_cnt[tid];
-        s_binc[tid] = (s_cnt[tid] + PB - 1) / PB;
-        s_minc[tid] = (s_cnt[tid] + MC - 1) / MC;
+        const int c = s_cnt[tid];
+        s_inc[tid] = c;
+        s_binc[tid] = (c + PB - 1) / PB;
+        s_finc[tid] = c / MC;
+        if (c % MC) atomicAdd(&s_bin[MC - c % MC], 1);
     }
     __syncthreads();
     for (int d = 1; d <= 256; d <<= 1) {
@@ -124,18 +142,32 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
         if (tid <= E && tid >= d) {
             a = s_inc[tid - d];
             b = s_binc[tid - d];
-            m = s_minc[tid - d];
+            m = s_finc[tid - d];
         }
         __syncthreads();
         if (tid <= E && tid >= d) {
             s_inc[tid] += a;
             s_binc[tid] += b;
-            s_minc[tid] += m;
+            s_finc[tid] += m;
         }
         __syncthreads();
     }
+    // exclusive prefix of the size bins (one wave; bin i holds chunks of
+    // MC - i pairs, so increasing i is decreasing size)
+    if (tid < MC) {
+        const int v = s_bin[tid];
+        int incl = v;
+#pragma unroll
+        for (int d = 1; d < MC; d <<= 1) {
+            const int o = __shfl_up(incl, d, MC);
+            if (tid >= d) incl += o;
+        }
+        s_bin[tid] = incl - v;
+        if (tid == MC - 1) s_nch = s_finc[E] + incl;
+    }
+    __syncthreads();
     if (tid <= E) {
-        int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2), *mco = tbo + (E + 2);
+        int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
         const int c = s_cnt[tid];
         s_off[tid] = s_inc[tid] - c;
         cnt[tid] = c;
@@ -143,13 +175,15 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
         const int nb = (c + PB - 1) / PB, b0 = s_binc[tid] - nb;
         tbo[tid] = b0;
         for (int i = 0; i < nb; i++) blk[b0 + i] = tid;
-        const int nm = (c + MC - 1) / MC, m0 = s_minc[tid] - nm;
-        mco[tid] = m0;
-        for (int i = 0; i < nm; i++) mblk[m0 + i] = tid;
+        const int nf = c / MC, f0 = s_finc[tid] - nf, o = s_inc[tid] - c;
+        for (int i = 0; i < nf; i++) chunk[f0 + i] = make_int4(tid, MC, o + i * MC, 0);
+        if (c % MC) {
+            const int bin = MC - c % MC;
+            chunk[s_finc[E] + s_bin[bin] + atomicAdd(&s_binf[bin], 1)] = make_int4(tid, c % MC, o + nf * MC, 0);
+        }
         if (tid == E) {
             off[E + 1] = s_inc[E];
             tbo[E + 1] = s_binc[E];
-            mco[E + 1] = s_minc[E];
         }
     }
     __syncthreads();
@@ -158,6 +192,7 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
         perm[s_off[e] + atomicAdd(&s_fill[e], 1)] = (p / K) * S + (p % K);
     }
     for (int t = tid; t < T; t += 1024) perm[s_off[E] + t] = t * S + K;
+    for (int i = s_nch + tid; i < max_chunks; i += 1024) chunk[i] = make_int4(-1, 0, 0, 0);
 }
 
 // LDS row stride of the staged activations: 16 bytes of padding move each
@@ -198,6 +233,17 @@ __device__ __forceinline__ void q4w_load(Q4W<CH> &w, const uint8_t *wrow, int c0
     }
 }
 
+template <int CH>
+__device__ __forceinline__ void q4w_opaque(Q4W<CH> &w)
+{
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        asm volatile("" : "+v"(w.hdr[c].x), "+v"(w.hdr[c].y), "+v"(w.hdr[c].z), "+v"(w.hdr[c].w));
+#pragma unroll
+        for (int g = 0; g < 4; g++) asm volatile("" : "+v"(w.qs[c][g].x), "+v"(w.qs[c][g].y));
+    }
+}
+
 template <int NB, int CH>
 __device__ __forceinline__ void q4w_mma(const Q4W<CH> &w, int c0, const int8_t *aq, const float *ad,
                                         float (&r)[4])
@@ -215,20 +261,46 @@ __device__ __forceinline__ void q4w_mma(const Q4W<CH> &w, int c0, const int8_t *
         int accs[4] = {0, 0, 0, 0};
         // min term: sum over the block of m(sub-block of k) * xq[k] -- an
         // MFMA against the mins broadcast over each sub-block, accumulated in
-        // the matrix core across the 8 sub-blocks (exact: int32)
+        // the matrix core across the block (exact: int32).  The K=64 form
+        // takes two sub-blocks: bytes 0-7 of a lane's operands are its k of
+        // sub-block 2t, bytes 8-15 its k of sub-block 2t+1, the same
+        // assignment for both operands, so the sum runs over exactly those k.
         v4i accm = {0, 0, 0, 0};
+        // per half block: four sub-block MFMAs back to back (independent),
+        // the two min MFMAs, then the scale multiply-adds on their results,
+        // so the matrix core stays busy while the VALU waits for the first
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const long a = *(const long *)(aq + lr * arow<NB>() + ib * QK_K + 32 * j + 8 * q);
-            const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, pack_nib(w.qs[c][j >> 1], j & 1),
-                                                                v4i{0, 0, 0, 0}, 0, 0, 0);
-            const int sc = (int)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 63);
-            const uint32_t mb = (((j < 4 ? m_lo : m_hi) >> (8 * (j & 3))) & 63) * 0x01010101u;
-            accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, (long)(((unsigned long long)mb << 32) | mb), accm, 0, 0, 0);
-            accs[0] += sc * p[0];
-            accs[1] += sc * p[1];
-            accs[2] += sc * p[2];
-            accs[3] += sc * p[3];
+        for (int hb = 0; hb < 2; hb++) {
+            long a[4];
+            v4i p[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int j = 4 * hb + jj;
+                a[jj] = *(const long *)(aq + lr * arow<NB>() + ib * QK_K + 32 * j + 8 * q);
+                p[jj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[jj], pack_nib(w.qs[c][j >> 1], j & 1),
+                                                              v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+            // mins of sub-blocks 4hb .. 4hb+3 are bytes 0-3 of m_lo / m_hi;
+            // each pair broadcast to all four bytes by one byte permute
+            const uint32_t mw = hb ? m_hi : m_lo;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint32_t m0 = __builtin_amdgcn_perm(0u, mw, 0x01010101u * (2 * t));
+                const uint32_t m1 = __builtin_amdgcn_perm(0u, mw, 0x01010101u * (2 * t + 1));
+                const v4i av = {(int)(uint32_t)a[2 * t], (int)(uint32_t)((unsigned long)a[2 * t] >> 32),
+                                (int)(uint32_t)a[2 * t + 1], (int)(uint32_t)((unsigned long)a[2 * t + 1] >> 32)};
+                accm = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, v4i{(int)m0, (int)m0, (int)m1, (int)m1}, accm, 0, 0,
+                                                             0);
+            }
+            const uint32_t sw = hb ? sc_hi : sc_lo;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int sc = (int)((sw >> (8 * jj)) & 63);
+                accs[0] = __mul24(sc, p[jj][0]) + accs[0];
+                accs[1] = __mul24(sc, p[jj][1]) + accs[1];
+                accs[2] = __mul24(sc, p[jj][2]) + accs[2];
+                accs[3] = __mul24(sc, p[jj][3]) + accs[3];
+            }
         }
         const float d = h2f(w.hdr[c].x & 0xffff), dmin = h2f(w.hdr[c].x >> 16);
         const float4 xd = *(const float4 *)(ad + ib * 16 + 4 * q);
@@ -297,10 +369,10 @@ __device__ __forceinline__ void q6w_mma(const Q6W<NB> &w, const int8_t *aq, cons
             const long a = *(const long *)(aq + lr * arow<NB>() + ib * QK_K + 128 * n + 32 * Q + 16 * hl + 8 * qq);
             const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
             const int sc = (int)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 255);
-            acc[0] += sc * p[0];
-            acc[1] += sc * p[1];
-            acc[2] += sc * p[2];
-            acc[3] += sc * p[3];
+            acc[0] = __mul24(sc, p[0]) + acc[0];
+            acc[1] = __mul24(sc, p[1]) + acc[1];
+            acc[2] = __mul24(sc, p[2]) + acc[2];
+            acc[3] = __mul24(sc, p[3]) + acc[3];
         }
         const float d = h2f(w.dbits[ib]);
         const float4 xd = *(const float4 *)(ad + ib * 16 + 4 * q);
@@ -333,172 +405,156 @@ __device__ __forceinline__ void stage_q8k(const int *s_pair, RowOf row_of, const
     }
 }
 
-// ------------------------------------------- gate / up, chunked streaming --
-// grid: (max MC-pair chunks) x (F / GU_RC); a workgroup = one chunk of up to
-// 64 pairs of one bucket x 64 gate rows and the same 64 up rows: waves 0-1
-// take the gate rows, 2-3 the up rows, 32 rows (2 MFMA row tiles) each.
-// The K loop runs over the NBE super-blocks with both operands double
-// buffered: the next block's weight bytes (registers) and Q8_K(x) rows
-// (loaded to registers, written to the other LDS buffer after the MFMAs)
-// are requested before the current block's MFMAs, so every wave streams
-// weights continuously (a block ahead: 6 KB per wave in flight, four
-// workgroups per CU) and each activation row is staged once per 64 rows.
-constexpr int GU_RC = 64;
-constexpr int GU_RT = 2;          // MFMA row tiles per wave
-constexpr int ARB = QK_K + 16;    // LDS bytes per staged pair row of one block (16 B pad vs bank conflicts)
+// --------------------------------------------- gate / up, rows resident --
+// grid: (max MC-pair chunks) x (F / GR_ROWS); a workgroup = one chunk of up
+// to 64 pairs of one bucket x 32 rows of h: waves 0-1 hold 16 gate rows
+// each, waves 2-3 the same rows of up.  A wave loads its 16 rows whole
+// (KH super-blocks = 1152 contiguous bytes per row for n_embd 2048) into
+// registers at once -- HBM sees each row read as one burst -- and keeps
+// them while the chunk's pairs stream past in M tiles of 16: the tile's
+// Q8_K(x) rows go global -> LDS by DMA (no registers), double buffered, the
+// next tile's DMA in flight during the current tile's MFMAs.  n_embd 4096
+// runs as two passes of 8 super-blocks.
+constexpr int GR_ROWS = 32;
 
-struct GUW {                      // a lane's bytes of one super-block of its GU_RT rows
-    uint4 hdr[GU_RT];
-    uint2 qs[GU_RT][4];
-};
-
-template <int NBE>
-__global__ __launch_bounds__(256, 2) void gateup_chunk_kernel(
-    const uint8_t *__restrict__ gate_exps, const uint8_t *__restrict__ up_exps,
-    const uint8_t *__restrict__ gate_sh, const uint8_t *__restrict__ up_sh, int E, int S, int F,
-    const int *__restrict__ grp, const int *__restrict__ mblk, const int *__restrict__ perm,
-    const int8_t *__restrict__ xq, const float *__restrict__ xd, float *__restrict__ h)
+// stage the Q8_K rows (super-blocks [kb0, kb0 + KH)) and scales of the M
+// tile's 16 tokens tok[0..15] into aq[16][arow<KH>()] / ad[KH][16].  The
+// DMAs are unconditional (an absent pair carries token 0, whose staged row
+// feeds only results that are never stored), so no branch separates them
+// and each wave's token reads batch into one LDS round trip.
+template <int KH>
+__device__ __forceinline__ void stage_dma(const int *tok, int nbe, int kb0, const int8_t *xq, const float *xd,
+                                          int8_t *aq, float *ad)
 {
-    __shared__ __align__(16) int8_t s_aq[2][MC * ARB];
-    __shared__ __align__(16) float s_ad[2][MC];
-    __shared__ int s_pair[MC];
-    const int rchunks = F / GU_RC;
-    const int u = (int)blockIdx.x / rchunks, rc = (int)blockIdx.x % rchunks;
-    const int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2), *mco = tbo + (E + 2);
-    if (u >= mco[E + 1]) return;
-    const int e = mblk[u], mc = u - mco[e];
-    const int npair = min(MC, cnt[e] - mc * MC), mtn = (npair + 15) / 16;
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), tid = (int)threadIdx.x;
-    const int lr = lane & 15, q = lane >> 4;
-    const int mat = wv >> 1, rbase = rc * GU_RC + 16 * GU_RT * (wv & 1);
-    constexpr size_t rowb = (size_t)NBE * Q4K_BYTES;
-    const uint8_t *W = mat == 0 ? (e < E ? gate_exps + (size_t)e * F * rowb : gate_sh)
-                                : (e < E ? up_exps + (size_t)e * F * rowb : up_sh);
-    if (tid < MC) s_pair[tid] = tid < npair ? perm[off[e] + mc * MC + tid] : -1;
-    __syncthreads();
-
-    auto w_load = [&](GUW &w, int kb) {
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
+    const size_t xrow = (size_t)nbe * QK_K;
+    if constexpr (KH >= 4) {
+        constexpr int PER = KH / 4;            // 1 KB pieces per staged row
 #pragma unroll
-        for (int rt = 0; rt < GU_RT; rt++) {
-            const uint8_t *blk = W + (size_t)(rbase + 16 * rt + lr) * rowb + (size_t)kb * Q4K_BYTES;
-            w.hdr[rt] = ld16(blk);
-#pragma unroll
-            for (int g = 0; g < 4; g++) w.qs[rt][g] = ld8(blk + 16 + 32 * g + 8 * q);
+        for (int i = wv; i < PB * PER; i += 4) {
+            const int p = i / PER, piece = i % PER;
+            __builtin_amdgcn_global_load_lds(
+                (const QMAG_GLOBAL void *)(xq + (size_t)tok[p] * xrow + (size_t)kb0 * QK_K + piece * 1024 + lane * 16),
+                (__attribute__((address_space(3))) void *)(aq + p * arow<KH>() + piece * 1024), 16, 0, 0);
         }
-    };
-    // one block of the chunk's Q8_K(x) rows: 64 rows x 16 parts of 16 bytes,
-    // 4 per thread, plus the 64 scales
-    uint4 sv[4];
-    float sd = 0.0f;
-    auto s_load = [&](int kb) {
+    } else {
+        constexpr int PER = KH;                // 256 B pieces, one dword per lane
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + 256 * i, p = c >> 4, part = c & 15, pr = s_pair[p];
-            sv[i] = pr >= 0 ? *(const uint4 *)(xq + (size_t)(pr / S) * (NBE * QK_K) + kb * QK_K + part * 16)
-                            : make_uint4(0, 0, 0, 0);
-        }
-        if (tid < MC) sd = s_pair[tid] >= 0 ? xd[(size_t)(s_pair[tid] / S) * NBE + kb] : 0.0f;
-    };
-    auto s_store = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + 256 * i, p = c >> 4, part = c & 15;
-            *(uint4 *)(&s_aq[buf][p * ARB + part * 16]) = sv[i];
-        }
-        if (tid < MC) s_ad[buf][tid] = sd;
-    };
-    float r[GU_RT][4][4];
-#pragma unroll
-    for (int rt = 0; rt < GU_RT; rt++)
-#pragma unroll
-        for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) r[rt][mt][i] = 0.0f;
-    auto compute = [&](const GUW &w, int buf) {
-        const int8_t *aq = s_aq[buf];
-#pragma unroll
-        for (int rt = 0; rt < GU_RT; rt++) {
-            // the 8 six-bit scales and mins of the row's block (src/q8k.c:22-30)
-            const uint32_t y = w.hdr[rt].y, z = w.hdr[rt].z, x4 = w.hdr[rt].w;
-            const uint32_t sc_lo = y & 0x3F3F3F3Fu, m_lo = z & 0x3F3F3F3Fu;
-            const uint32_t sc_hi = (x4 & 0x0F0F0F0Fu) | (((y >> 6) & 0x03030303u) << 4);
-            const uint32_t m_hi = ((x4 >> 4) & 0x0F0F0F0Fu) | (((z >> 6) & 0x03030303u) << 4);
-            const float d = h2f(w.hdr[rt].x & 0xffff), dmin = h2f(w.hdr[rt].x >> 16);
-#pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
-                if (mt < mtn) {                  // workgroup-uniform
-                    int acc[4] = {0, 0, 0, 0};
-                    v4i accm = {0, 0, 0, 0};
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const long a = *(const long *)(aq + (16 * mt + lr) * ARB + 32 * j + 8 * q);
-                        const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, pack_nib(w.qs[rt][j >> 1], j & 1),
-                                                                            v4i{0, 0, 0, 0}, 0, 0, 0);
-                        const int sc = (int)(((j < 4 ? sc_lo : sc_hi) >> (8 * (j & 3))) & 63);
-                        const uint32_t mb = (((j < 4 ? m_lo : m_hi) >> (8 * (j & 3))) & 63) * 0x01010101u;
-                        accm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, (long)(((unsigned long long)mb << 32) | mb),
-                                                                     accm, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; i++) acc[i] += sc * p[i];
-                    }
-                    const float4 xs = *(const float4 *)(s_ad[buf] + 16 * mt + 4 * q);
-                    r[rt][mt][0] += (d * xs.x) * (float)acc[0] - (dmin * xs.x) * (float)accm[0];
-                    r[rt][mt][1] += (d * xs.y) * (float)acc[1] - (dmin * xs.y) * (float)accm[1];
-                    r[rt][mt][2] += (d * xs.z) * (float)acc[2] - (dmin * xs.z) * (float)accm[2];
-                    r[rt][mt][3] += (d * xs.w) * (float)acc[3] - (dmin * xs.w) * (float)accm[3];
-                }
-            }
-        }
-    };
-
-    GUW wa, wb;
-    w_load(wa, 0);
-    s_load(0);
-    s_store(0);
-    __syncthreads();
-    for (int kb = 0; kb < NBE; kb += 2) {
-        // block kb from (wa, buffer 0) while block kb+1 streams into (wb, buffer 1)
-        if (kb + 1 < NBE) {
-            w_load(wb, kb + 1);
-            s_load(kb + 1);
-        }
-        compute(wa, 0);
-        if (kb + 1 < NBE) s_store(1);
-        __syncthreads();
-        if (kb + 1 < NBE) {
-            if (kb + 2 < NBE) {
-                w_load(wa, kb + 2);
-                s_load(kb + 2);
-            }
-            compute(wb, 1);
-            if (kb + 2 < NBE) s_store(0);
-            __syncthreads();
+        for (int i = wv; i < PB * PER; i += 4) {
+            const int p = i / PER, piece = i % PER;
+            __builtin_amdgcn_global_load_lds(
+                (const QMAG_GLOBAL void *)(xq + (size_t)tok[p] * xrow + (size_t)kb0 * QK_K + piece * 256 + lane * 4),
+                (__attribute__((address_space(3))) void *)(aq + p * arow<KH>() + piece * 256), 4, 0, 0);
         }
     }
-    // h = silu(g) * u: the up waves hand their results to the gate waves
-    // through LDS (the activation buffers are free now)
-    float *ex = (float *)&s_aq[0][0];
-    auto exi = [&](int rt, int mt, int i) { return ((((wv & 1) * GU_RT + rt) * 4 + mt) * 4 + i) * 64 + lane; };
+    // scales, ad[c][p]: thread t -> block c = t / 16, pair p = t % 16; the
+    // lanes past the KH * 16 scales stay masked (their DMA slot would lie
+    // beyond ad)
+    if (wv * 64 < PB * KH) {
+        const int t = wv * 64 + lane, c = t / PB, p = t % PB;
+        if (t < PB * KH)
+            __builtin_amdgcn_global_load_lds((const QMAG_GLOBAL void *)(xd + (size_t)tok[p] * nbe + kb0 + c),
+                                             (__attribute__((address_space(3))) void *)(ad + wv * 64), 4, 0, 0);
+    }
+}
+
+template <int NBE>
+__global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
+    const uint8_t *__restrict__ gate_exps, const uint8_t *__restrict__ up_exps,
+    const uint8_t *__restrict__ gate_sh, const uint8_t *__restrict__ up_sh, int E, int S, int F,
+    const int4 *__restrict__ chunk, const int *__restrict__ perm,
+    const int8_t *__restrict__ xq, const float *__restrict__ xd, float *__restrict__ h)
+{
+    constexpr int KH = NBE < 8 ? NBE : 8;      // super-blocks held per pass
+    constexpr int NPASS = NBE / KH;
+    // the two buffers are separate LDS objects: the compiler then knows
+    // that reading one need not wait for the DMA into the other
+    __shared__ __align__(16) int8_t s_aq0[PB * arow<KH>()], s_aq1[PB * arow<KH>()];
+    __shared__ __align__(16) float s_ad0[KH * PB], s_ad1[KH * PB];
+    __shared__ int s_pair[MC], s_tok[MC];
+    const int rchunks = F / GR_ROWS;
+    const int u = (int)blockIdx.x / rchunks, rc = (int)blockIdx.x % rchunks;
+    const int4 ck = chunk[u];
+    if (ck.x < 0) return;
+    const int e = ck.x, npair = ck.y, mtn = (npair + PB - 1) / PB;
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
+    const int lr = lane & 15, q = lane >> 4, mat = wv >> 1;
+    const int row0 = rc * GR_ROWS + 16 * (wv & 1);
+    constexpr size_t rowb = (size_t)NBE * Q4K_BYTES;
+    const uint8_t *wrow = (mat == 0 ? (e < E ? gate_exps + (size_t)e * F * rowb : gate_sh)
+                                    : (e < E ? up_exps + (size_t)e * F * rowb : up_sh)) +
+                          (size_t)(row0 + lr) * rowb;
+    // the weight rows go out first; the pair ids follow as scalar loads
+    // (their own counter), so waiting for them leaves the weights in flight
+    Q4W<KH> w;
+    q4w_load(w, wrow, 0);
+    {
+        const int wvu = __builtin_amdgcn_readfirstlane(wv);
+        const int base = ck.z + 16 * wvu, last = ck.z + npair - 1;
+        int v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = perm[min(base + k, last)];
+        int mine = -1;
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (lane == k && 16 * wvu + k < npair) mine = v[k];
+        if (lane < 16) {
+            s_pair[16 * wvu + lane] = mine;
+            s_tok[16 * wvu + lane] = mine >= 0 ? mine / S : 0;
+        }
+    }
+    __syncthreads();
+
+    float r[MC / PB][4];
+#pragma unroll
+    for (int m = 0; m < MC / PB; m++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[m][i] = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ps++) {
+        if (ps > 0) q4w_load(w, wrow, ps * KH);
+        stage_dma<KH>(s_tok, NBE, ps * KH, xq, xd, s_aq0, s_ad0);
+#pragma unroll
+        for (int m = 0; m < MC / PB; m++) {
+            if (m < mtn) {                     // workgroup-uniform
+                // tile m has landed (the barrier waits for this wave's DMA,
+                // then for every wave) and tile m-1's buffer is free
+                __syncthreads();
+                if (m + 1 < mtn)
+                    stage_dma<KH>(s_tok + PB * (m + 1), NBE, ps * KH, xq, xd, (m & 1) ? s_aq0 : s_aq1,
+                                  (m & 1) ? s_ad0 : s_ad1);
+                // the weight registers are opaque to the compiler from here,
+                // so it derives the MFMA operands anew per tile instead of
+                // keeping all of them (twice the registers) live across tiles
+                q4w_opaque(w);
+                q4w_mma<KH, KH>(w, 0, (m & 1) ? s_aq1 : s_aq0, (m & 1) ? s_ad1 : s_ad0, r[m]);
+            }
+        }
+        __syncthreads();                       // the buffers are free for the next pass / the hand-off
+    }
+    // h = silu(g) * u: the up waves hand their sums to the gate waves
+    // through LDS
+    float *ex = (float *)s_aq0;
+    auto exi = [&](int m, int i) { return (((wv & 1) * (MC / PB) + m) * 4 + i) * 64 + lane; };
     if (mat == 1) {
 #pragma unroll
-        for (int rt = 0; rt < GU_RT; rt++)
+        for (int m = 0; m < MC / PB; m++)
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) ex[exi(rt, mt, i)] = r[rt][mt][i];
+            for (int i = 0; i < 4; i++)
+                if (m < mtn) ex[exi(m, i)] = r[m][i];
     }
     __syncthreads();
     if (mat == 0) {
 #pragma unroll
-        for (int rt = 0; rt < GU_RT; rt++)
+        for (int m = 0; m < MC / PB; m++)
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int pr = s_pair[16 * mt + 4 * q + i];
-                    const float g = r[rt][mt][i], uu = ex[exi(rt, mt, i)];
-                    if (mt < mtn && pr >= 0) h[(size_t)pr * F + rbase + 16 * rt + lr] = (g / (1.0f + expf(-g))) * uu;
+            for (int i = 0; i < 4; i++) {
+                const int pr = s_pair[PB * m + 4 * q + i];
+                if (m < mtn && pr >= 0) {
+                    const float g = r[m][i], uu = ex[exi(m, i)];
+                    h[(size_t)pr * F + row0 + lr] = (g / (1.0f + expf(-g))) * uu;
                 }
+            }
     }
 }
 
@@ -587,12 +643,12 @@ int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *lo
 }
 
 template <int NBE>
-static void launch_gu(const qmag_moe_layer *L, int S, int max_chunks, const int *grp, const int *mblk,
+static void launch_gu(const qmag_moe_layer *L, int S, int max_chunks, const int4 *chunk,
                       const int *perm, const int8_t *xq, const float *xd, float *h, hipStream_t s)
 {
-    hipLaunchKernelGGL(gateup_chunk_kernel<NBE>, dim3(max_chunks * (L->n_ff / GU_RC)), dim3(256), 0, s,
+    hipLaunchKernelGGL(gateup_rows_kernel<NBE>, dim3(max_chunks * (L->n_ff / GR_ROWS)), dim3(256), 0, s,
                        (const uint8_t *)L->gate_exps, (const uint8_t *)L->up_exps, (const uint8_t *)L->gate_shexp,
-                       (const uint8_t *)L->up_shexp, L->n_expert, S, L->n_ff, grp, mblk, perm, xq, xd, h);
+                       (const uint8_t *)L->up_shexp, L->n_expert, S, L->n_ff, chunk, perm, xq, xd, h);
 }
 
 template <int NBF>
@@ -614,23 +670,25 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
     // ceil(n_e / 16) <= T*K/16 + E, plus the shared bucket
     const int max_blocks = (T * K + PB - 1) / PB + E + (T + PB - 1) / PB;
     const int max_chunks = (T * K + MC - 1) / MC + E + (T + MC - 1) / MC;
-    int *grp = (int *)workspace(WS_GRP, sizeof(int) * ((size_t)4 * (E + 2) + max_blocks + max_chunks + (size_t)T * S),
-                                &st);
+    // int4 chunk descriptors first (16-byte aligned), then the int tables
+    int4 *chunk = (int4 *)workspace(WS_GRP, sizeof(int4) * (size_t)max_chunks +
+                                                sizeof(int) * ((size_t)4 * (E + 2) + max_blocks + (size_t)T * S),
+                                    &st);
     if (st) return st;
-    int *blk = grp + 4 * (E + 2), *mblk = blk + max_blocks, *perm = mblk + max_chunks;
+    int *grp = (int *)(chunk + max_chunks), *blk = grp + 4 * (E + 2), *perm = blk + max_blocks;
     float *y = (float *)workspace(WS_Y, sizeof(float) * (size_t)T * S * N, &st);
     if (st) return st;
 
     prof_begin(PROF_GROUP, s);
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, sel, T, K, E, grp, blk, mblk, perm);
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, sel, T, K, E, grp, blk, chunk, max_chunks, perm);
     prof_end(PROF_GROUP, s);
     prof_begin(PROF_GATEUP, s);
     switch (N / QK_K) {
-    case 1: launch_gu<1>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
-    case 2: launch_gu<2>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
-    case 4: launch_gu<4>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
-    case 8: launch_gu<8>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
-    default: launch_gu<16>(L, S, max_chunks, grp, mblk, perm, xq, xd, h, s); break;
+    case 1: launch_gu<1>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
+    case 2: launch_gu<2>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
+    case 4: launch_gu<4>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
+    case 8: launch_gu<8>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
+    default: launch_gu<16>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
     }
     prof_end(PROF_GATEUP, s);
     prof_begin(PROF_HQUANT, s);
