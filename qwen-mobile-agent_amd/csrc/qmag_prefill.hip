@@ -383,6 +383,82 @@ __device__ __forceinline__ void q6w_mma(const Q6W<NB> &w, const int8_t *aq, cons
     }
 }
 
+// The same rows with every group's MFMA operand built once (centred 6-bit
+// values, lanes q = 2, 3 zero): a workgroup that runs several M tiles
+// against the same rows unpacks them once instead of per tile.
+template <int NB>
+struct Q6B {
+    long b[NB][16];
+    uint4 sc16[NB];
+    uint32_t dbits[NB];
+};
+
+template <int NB>
+__device__ __forceinline__ void q6b_unpack(Q6B<NB> &u, const Q6W<NB> &w)
+{
+    const int q = lane_id() >> 4;
+#pragma unroll
+    for (int ib = 0; ib < NB; ib++) {
+        u.sc16[ib] = w.sc16[ib];
+        u.dbits[ib] = w.dbits[ib];
+#pragma unroll
+        for (int gg = 0; gg < 16; gg++) {
+            const int n = gg >> 3, Q = (gg >> 1) & 3, hl = gg & 1;
+            const uint2 l8 = w.ql[ib][n][hl][Q & 1], h8 = w.qh[ib][n][hl];
+            const uint32_t lo0 = Q < 2 ? l8.x & 0x0F0F0F0Fu : (l8.x >> 4) & 0x0F0F0F0Fu;
+            const uint32_t lo1 = Q < 2 ? l8.y & 0x0F0F0F0Fu : (l8.y >> 4) & 0x0F0F0F0Fu;
+            const uint32_t hb0 = ((h8.x >> (2 * Q)) & 0x03030303u) << 4;
+            const uint32_t hb1 = ((h8.y >> (2 * Q)) & 0x03030303u) << 4;
+            u.b[ib][gg] = q < 2 ? (long)(((unsigned long long)q6_center(lo1 | hb1) << 32) | q6_center(lo0 | hb0)) : 0;
+        }
+    }
+}
+
+template <int NB>
+__device__ __forceinline__ void q6b_opaque(Q6B<NB> &u)
+{
+#pragma unroll
+    for (int ib = 0; ib < NB; ib++)
+#pragma unroll
+        for (int gg = 0; gg < 16; gg++) asm volatile("" : "+v"(u.b[ib][gg]));
+}
+
+template <int NB>
+__device__ __forceinline__ void q6b_mma(const Q6B<NB> &u, const int8_t *aq, const float *ad, float (&r)[4])
+{
+    const int lane = lane_id(), lr = lane & 15, q = lane >> 4, qq = q & 1;
+#pragma unroll
+    for (int ib = 0; ib < NB; ib++) {
+        int acc[4] = {0, 0, 0, 0};
+        const uint32_t scw[4] = {u.sc16[ib].x, u.sc16[ib].y, u.sc16[ib].z, u.sc16[ib].w};
+#pragma unroll
+        for (int h4 = 0; h4 < 4; h4++) {
+            // four groups' MFMAs back to back, then their scale multiply-adds
+            v4i p[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int gg = 4 * h4 + g, n = gg >> 3, Q = (gg >> 1) & 3, hl = gg & 1;
+                const long a = *(const long *)(aq + lr * arow<NB>() + ib * QK_K + 128 * n + 32 * Q + 16 * hl + 8 * qq);
+                p[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, u.b[ib][gg], v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int sc = (int)(int8_t)((scw[h4] >> (8 * g)) & 255);
+                acc[0] = __mul24(sc, p[g][0]) + acc[0];
+                acc[1] = __mul24(sc, p[g][1]) + acc[1];
+                acc[2] = __mul24(sc, p[g][2]) + acc[2];
+                acc[3] = __mul24(sc, p[g][3]) + acc[3];
+            }
+        }
+        const float d = h2f(u.dbits[ib]);
+        const float4 xd = *(const float4 *)(ad + ib * 16 + 4 * q);
+        r[0] += d * xd.x * (float)acc[0];
+        r[1] += d * xd.y * (float)acc[1];
+        r[2] += d * xd.z * (float)acc[2];
+        r[3] += d * xd.w * (float)acc[3];
+    }
+}
+
 // Stage the Q8_K rows of the block's pairs into LDS (zeros for missing
 // pairs).  src rows are indexed by `row_of(pair)`; NB blocks of 256 each.
 // (The Q4_K min term is taken by the matrix core from the staged xq, so the
@@ -559,62 +635,136 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
 }
 
 // ----------------------------------------------------------------- down --
-// grid: (max 16-pair blocks) x (N / 64); y[pair][row] = row . Q8_K(h[pair]),
-// 16 rows per wave; the weight loads are issued before the staging.
+// grid: (max MC-pair chunks) x (N / 64); a workgroup = one chunk of up to 64
+// pairs of one bucket x 64 rows, 16 per wave.  Each wave loads its rows
+// whole (NBF super-blocks, 420 contiguous bytes per Q6_K row for n_ff 512)
+// into registers, the chunk's Q8_K(h) rows are staged in LDS at once by
+// DMA, and y[pair][row] = row . Q8_K(h[pair]) runs M tile by M tile.
+constexpr int DN_ROWS = 64;
+
+template <int NB>
+__device__ __forceinline__ void q6w_opaque(Q6W<NB> &w)
+{
+#pragma unroll
+    for (int ib = 0; ib < NB; ib++) {
+        asm volatile("" : "+v"(w.sc16[ib].x), "+v"(w.sc16[ib].y), "+v"(w.sc16[ib].z), "+v"(w.sc16[ib].w),
+                     "+v"(w.dbits[ib]));
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int hl = 0; hl < 2; hl++)
+                asm volatile("" : "+v"(w.ql[ib][n][hl][0].x), "+v"(w.ql[ib][n][hl][0].y), "+v"(w.ql[ib][n][hl][1].x),
+                             "+v"(w.ql[ib][n][hl][1].y), "+v"(w.qh[ib][n][hl].x), "+v"(w.qh[ib][n][hl].y));
+    }
+}
+
+// stage rows[0 .. 16*mtn) of Q8_K(h) (NB super-blocks each) into
+// aq[p][arow<NB>()] and their scales into ad[p / 16][block][p % 16]: one
+// 256-byte DMA per (pair, block), one dword per lane; every pair slot has a
+// valid row (absent pairs repeat the chunk's first), so no DMA is skipped
+template <int NB>
+__device__ __forceinline__ void stage_rows_dma(const int *rows, int mtn, const int8_t *hq, const float *hd,
+                                               int8_t *aq, float *ad)
+{
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
+    const int n = PB * mtn * NB;
+    for (int i = wv; i < n; i += 4) {          // wave-uniform
+        const int p = i / NB, ib = i % NB;
+        __builtin_amdgcn_global_load_lds(
+            (const QMAG_GLOBAL void *)(hq + (size_t)rows[p] * (NB * QK_K) + ib * QK_K + lane * 4),
+            (__attribute__((address_space(3))) void *)(aq + p * arow<NB>() + ib * QK_K), 4, 0, 0);
+    }
+    for (int s0 = 64 * wv; s0 < n; s0 += 256) {
+        const int sl = s0 + lane, mt = sl / (NB * PB), ib = (sl / PB) % NB, p = PB * mt + sl % PB;
+        if (sl < n)
+            __builtin_amdgcn_global_load_lds((const QMAG_GLOBAL void *)(hd + (size_t)rows[min(p, PB * mtn - 1)] * NB + ib),
+                                             (__attribute__((address_space(3))) void *)(ad + s0), 4, 0, 0);
+    }
+}
+
 template <int NBF, int TD>
-__device__ __forceinline__ void down_rows(const uint8_t *D, const int8_t *aq, const float *ad,
-                                          const int *s_pair, float (&r)[4])
+__device__ __forceinline__ void down_tiles(const uint8_t *D, const int8_t *aq, const float *ad, int mtn,
+                                           float (&r)[MC / PB][4])
 {
     if constexpr (TD == QMAG_TYPE_Q6_K) {
-        Q6W<NBF> w;
-        q6w_load(w, D);
-        __syncthreads();          // the staging (issued by the caller) is complete
-        q6w_mma<NBF>(w, aq, ad, r);
+        Q6B<NBF> u;
+        {
+            Q6W<NBF> w;
+            q6w_load(w, D);
+            q6b_unpack(u, w);
+        }
+        __syncthreads();                       // the staging DMA has landed (every wave's)
+#pragma unroll
+        for (int m = 0; m < MC / PB; m++)
+            if (m < mtn) {
+                q6b_opaque(u);
+                q6b_mma<NBF>(u, aq + PB * m * arow<NBF>(), ad + m * NBF * PB, r[m]);
+            }
     } else {
         Q4W<NBF> w;
         q4w_load(w, D, 0);
         __syncthreads();
-        q4w_mma<NBF, NBF>(w, 0, aq, ad, r);
+#pragma unroll
+        for (int m = 0; m < MC / PB; m++)
+            if (m < mtn) {
+                q4w_opaque(w);
+                q4w_mma<NBF, NBF>(w, 0, aq + PB * m * arow<NBF>(), ad + m * NBF * PB, r[m]);
+            }
     }
 }
 
 template <int NBF>
-__global__ __launch_bounds__(256, 2) void down_grouped_kernel(
+__global__ __launch_bounds__(256, 2) void down_rows_kernel(
     const uint8_t *__restrict__ down_exps, int t_down, const uint8_t *__restrict__ down_sh, int t_down_sh,
-    int E, int N, const int *__restrict__ grp, const int *__restrict__ blk, const int *__restrict__ perm,
-    const int8_t *__restrict__ hq, const float *__restrict__ hd, const int16_t *__restrict__ hs,
-    float *__restrict__ y)
+    int E, int N, const int4 *__restrict__ chunk, const int *__restrict__ perm, const int8_t *__restrict__ hq,
+    const float *__restrict__ hd, float *__restrict__ y)
 {
-    __shared__ __align__(16) int8_t s_aq[PB * arow<NBF>()];
-    __shared__ __align__(16) float s_ad[NBF * PB];
-    __shared__ int s_pair[PB];
-    const int rblocks = N / 64;
-    const int tbg = (int)blockIdx.x / rblocks, rb = (int)blockIdx.x % rblocks;
-    const int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
-    if (tbg >= tbo[E + 1]) return;
-    const int e = blk[tbg];
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), lr = lane & 15, q = lane >> 4;
-    const int row = rb * 64 + wv * 16 + lr;
-    const int ltb = tbg - tbo[e];
-    if (threadIdx.x < PB) {
-        const int i = PB * ltb + (int)threadIdx.x;
-        s_pair[threadIdx.x] = i < cnt[e] ? perm[off[e] + i] : -1;
+    __shared__ __align__(16) int8_t s_aq[MC * arow<NBF>()];
+    __shared__ __align__(16) float s_ad[MC * NBF];
+    __shared__ int s_pair[MC], s_row[MC];
+    const int rblocks = N / DN_ROWS;
+    const int u = (int)blockIdx.x / rblocks, rb = (int)blockIdx.x % rblocks;
+    const int4 ck = chunk[u];
+    if (ck.x < 0) return;
+    const int e = ck.x, npair = ck.y, mtn = (npair + PB - 1) / PB;
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), q = lane >> 4;
+    const int row = rb * DN_ROWS + wv * 16 + (lane & 15);
+    // pair ids by scalar loads (see gateup_rows_kernel); rows of absent
+    // pairs repeat the first pair's
+    {
+        const int wvu = __builtin_amdgcn_readfirstlane(wv);
+        const int base = ck.z + 16 * wvu, last = ck.z + npair - 1;
+        int v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = perm[min(base + k, last)];
+        int mine = -1;
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (lane == k && 16 * wvu + k < npair) mine = v[k];
+        if (lane < 16) {
+            s_pair[16 * wvu + lane] = mine;
+            s_row[16 * wvu + lane] = mine >= 0 ? mine : perm[ck.z];
+        }
     }
     __syncthreads();
-    // the staging loads go out first; each wave then issues its weight
-    // loads and waits at the barrier inside down_rows
-    stage_q8k<NBF>(s_pair, [&](int pr) { return pr; }, hq, hd, s_aq, s_ad);
+    stage_rows_dma<NBF>(s_row, mtn, hq, hd, s_aq, s_ad);
     const int td = e < E ? t_down : t_down_sh;
     const size_t rowb = (size_t)NBF * (td == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES);
     const uint8_t *D = (e < E ? down_exps + (size_t)e * N * rowb : down_sh) + row * rowb;
-    float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (td == QMAG_TYPE_Q6_K) down_rows<NBF, QMAG_TYPE_Q6_K>(D, s_aq, s_ad, s_pair, r);
-    else down_rows<NBF, QMAG_TYPE_Q4_K>(D, s_aq, s_ad, s_pair, r);
+    float r[MC / PB][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int pr = s_pair[4 * q + i];
-        if (pr >= 0) y[(size_t)pr * N + row] = r[i];
-    }
+    for (int m = 0; m < MC / PB; m++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[m][i] = 0.0f;
+    if (td == QMAG_TYPE_Q6_K) down_tiles<NBF, QMAG_TYPE_Q6_K>(D, s_aq, s_ad, mtn, r);
+    else down_tiles<NBF, QMAG_TYPE_Q4_K>(D, s_aq, s_ad, mtn, r);
+#pragma unroll
+    for (int m = 0; m < MC / PB; m++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int pr = s_pair[PB * m + 4 * q + i];
+            if (m < mtn && pr >= 0) y[(size_t)pr * N + row] = r[m][i];
+        }
 }
 
 // -------------------------------------------------------------- combine --
@@ -652,12 +802,12 @@ static void launch_gu(const qmag_moe_layer *L, int S, int max_chunks, const int4
 }
 
 template <int NBF>
-static void launch_dn(const qmag_moe_layer *L, int max_blocks, const int *grp, const int *blk,
-                      const int *perm, const int8_t *hq, const float *hd, const int16_t *hs, float *y, hipStream_t s)
+static void launch_dn(const qmag_moe_layer *L, int max_chunks, const int4 *chunk, const int *perm, const int8_t *hq,
+                      const float *hd, float *y, hipStream_t s)
 {
-    hipLaunchKernelGGL(down_grouped_kernel<NBF>, dim3(max_blocks * (L->n_embd / 64)), dim3(256), 0, s,
+    hipLaunchKernelGGL(down_rows_kernel<NBF>, dim3(max_chunks * (L->n_embd / DN_ROWS)), dim3(256), 0, s,
                        (const uint8_t *)L->down_exps, L->t_down_exps, (const uint8_t *)L->down_shexp,
-                       L->t_down_shexp, L->n_expert, L->n_embd, grp, blk, perm, hq, hd, hs, y);
+                       L->t_down_shexp, L->n_expert, L->n_embd, chunk, perm, hq, hd, y);
 }
 
 int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, const float *gs,
@@ -697,9 +847,9 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
     if (st) return st;
     prof_begin(PROF_DOWN, s);
     switch (F / QK_K) {
-    case 1: launch_dn<1>(L, max_blocks, grp, blk, perm, hq, hd, hs, y, s); break;
-    case 2: launch_dn<2>(L, max_blocks, grp, blk, perm, hq, hd, hs, y, s); break;
-    default: launch_dn<4>(L, max_blocks, grp, blk, perm, hq, hd, hs, y, s); break;
+    case 1: launch_dn<1>(L, max_chunks, chunk, perm, hq, hd, y, s); break;
+    case 2: launch_dn<2>(L, max_chunks, chunk, perm, hq, hd, y, s); break;
+    default: launch_dn<4>(L, max_chunks, chunk, perm, hq, hd, y, s); break;
     }
     prof_end(PROF_DOWN, s);
     prof_begin(PROF_COMBINE, s);
