@@ -42,26 +42,26 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int PB = 16;            // pairs per MFMA tile (the 16-wide M side)
 
 // --------------------------------------------------------------- router --
-// One wave per 16 tokens x 16 experts; lane group q = lane / 16 owns the
-// k range [q*N/4, (q+1)*N/4), so each lane streams its own contiguous slice
-// of one x row and one router row.
+// One workgroup per 16 tokens x 16 experts; its four waves split k four
+// ways and lane group q of a wave owns a contiguous sixteenth of k, so each
+// lane streams its own slice of one x row and one router row (float4
+// loads, four independent accumulators).  The four waves' partial tiles
+// are summed through LDS in a fixed order.
 __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restrict__ Wr,
                                                           const float *__restrict__ bias,
                                                           const float *__restrict__ x, int N, int E,
                                                           int T, float *__restrict__ logits)
 {
-    const int lane = lane_id();
-    const int wave = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+    __shared__ v4f s_red[3][64];
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
     const int eblocks = (E + 15) / 16;
-    const int tb = wave / eblocks, eb = wave % eblocks;
+    const int tb = (int)blockIdx.x / eblocks, eb = (int)blockIdx.x % eblocks;
     if (tb * 16 >= T) return;
     const int tok = tb * 16 + (lane & 15), e = eb * 16 + (lane & 15), q = lane >> 4;
-    const int seg = N / 4;
-    const float4 *xr = (const float4 *)(x + (size_t)(tok < T ? tok : 0) * N + q * seg);
-    const float4 *wr = (const float4 *)(Wr + (size_t)(e < E ? e : 0) * N + q * seg);
+    const int seg = N / 16;                    // k per lane
+    const float4 *xr = (const float4 *)(x + (size_t)(tok < T ? tok : 0) * N + (4 * wv + q) * seg);
+    const float4 *wr = (const float4 *)(Wr + (size_t)(e < E ? e : 0) * N + (4 * wv + q) * seg);
     const float xs = tok < T ? 1.0f : 0.0f, ws = e < E ? 1.0f : 0.0f;
-    // four independent accumulators, each fed from its own float4 of the
-    // slice; 4 float4 of x and of Wr in flight per lane per step
     v4f acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
                   {0.0f, 0.0f, 0.0f, 0.0f}};
     for (int s = 0; s < seg / 4; s += 4) {
@@ -79,7 +79,11 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
             acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w * xs, b[u].w * ws, acc[u], 0, 0, 0);
         }
     }
-    const v4f sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    const v4f part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    if (wv > 0) s_red[wv - 1][lane] = part;
+    __syncthreads();
+    if (wv > 0) return;
+    const v4f sum = (part + s_red[0][lane]) + (s_red[1][lane] + s_red[2][lane]);
     // lane holds logits[tb*16 + 4q + i][eb*16 + lane%16]
     const int eo = eb * 16 + (lane & 15);
 #pragma unroll
@@ -785,8 +789,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *logits, hipStream_t s)
 {
     const int N = L->n_embd, E = L->n_expert;
-    const int waves = ((T + 15) / 16) * ((E + 15) / 16);
-    hipLaunchKernelGGL(router_mfma_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, L->gate_inp, L->router_bias,
+    const int tiles = ((T + 15) / 16) * ((E + 15) / 16);
+    hipLaunchKernelGGL(router_mfma_kernel, dim3(tiles), dim3(256), 0, s, L->gate_inp, L->router_bias,
                        x, N, E, T, logits);
     QMAG_HIP(hipGetLastError());
     return QMAG_OK;
