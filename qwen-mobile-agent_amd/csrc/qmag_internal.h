@@ -43,6 +43,7 @@ enum WsSlot {
     WS_FLAGS,                       // kernel status / counters
     WS_GRP,                         // grouped prefill: bucket counts/offsets, pair permutation
     WS_Y,                           // grouped prefill: per-pair down outputs
+    WS_XMB,                         // grouped prefill: Q8_K(x) sub-block sums times the block scale
     WS_COUNT
 };
 void *workspace(int slot, size_t bytes, int *status);
@@ -69,7 +70,7 @@ int moe_check_layer(const qmag_moe_layer *L);
 // grouped prefill (qmag_prefill.hip)
 int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *logits, hipStream_t s);
 int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, const float *gs,
-                const int8_t *xq, const float *xd, const int16_t *xs, float *h, int8_t *hq, float *hd,
+                const int8_t *xq, const float *xd, const float *xmb, float *h, int8_t *hq, float *hd,
                 int16_t *hs, const float *resid, float *out, hipStream_t s);
 
 // persistent single-launch decode (qmag_fused.hip)

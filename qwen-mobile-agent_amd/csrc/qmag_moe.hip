@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
                                                    float *__restrict__ wout,
                                                    float *__restrict__ gs_out,
                                                    int8_t *__restrict__ xq, float *__restrict__ xd,
-                                                   int16_t *__restrict__ xs)
+                                                   int16_t *__restrict__ xs, float *__restrict__ xmb)
 {
     __shared__ int8_t s_xq[4096];
     __shared__ float s_xd[16];
@@ -73,6 +73,10 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
             s_xd[b] = r.d;
         }
         if ((lane & 3) == 0) xs[(size_t)t * (N / 16) + b * 16 + (lane >> 2)] = (int16_t)r.gsum;
+        // the grouped prefill's Q4_K min-term operand: d * (sum of the 32
+        // values of each sub-block), lanes 8j .. 8j+7 holding sub-block j
+        const int s32 = r.gsum + __shfl_xor(r.gsum, 4);
+        if (xmb && (lane & 7) == 0) xmb[(size_t)t * (N / 32) + b * 8 + (lane >> 3)] = r.d * (float)s32;
     }
 
     if (wv == 0) {
@@ -321,7 +325,7 @@ struct MoeWs {
     float *logits, *w, *gs, *h, *hd;
     int *sel;
     int8_t *xq, *hq;
-    float *xd;
+    float *xd, *xmb;
     int16_t *xs, *hs;
 };
 
@@ -339,6 +343,7 @@ static int moe_ws(const qmag_moe_layer *L, int T, MoeWs &ws)
     WS(xq, int8_t, WS_XQ, (size_t)T * N);
     WS(xd, float, WS_XD, (size_t)T * (N / QK_K));
     WS(xs, int16_t, WS_XS, (size_t)T * (N / 16));
+    WS(xmb, float, WS_XMB, (size_t)T * (N / 32));
     WS(h, float, WS_H, (size_t)T * S * F);
     WS(hq, int8_t, WS_HQ, (size_t)T * S * F);
     WS(hd, float, WS_HD, (size_t)T * S * (F / QK_K));
@@ -416,10 +421,11 @@ int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const fl
     prof_end(PROF_ROUTER, s);
     prof_begin(PROF_TOPK, s);
     hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(256), 0, s, ws.logits, x, L->gate_inp_shexp, N,
-                       E, K, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs);
+                       E, K, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs, grouped ? ws.xmb : nullptr);
     prof_end(PROF_TOPK, s);
     if (grouped) {
-        st = moe_grouped(L, T, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs, ws.h, ws.hq, ws.hd, ws.hs, resid, out, s);
+        st = moe_grouped(L, T, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xmb, ws.h, ws.hq, ws.hd, ws.hs, resid, out,
+                         s);
         if (st) return st;
         g_last = ws;
         g_last_K = K;

@@ -315,6 +315,65 @@ __device__ __forceinline__ void q4w_mma(const Q4W<CH> &w, int c0, const int8_t *
     }
 }
 
+// Same contract, with the min term taken from a precomputed operand:
+// amb[(c*2 + h)*64 + 16*k + p] = xd_c(pair p) * (sum of sub-block 4h + k of
+// pair p's Q8_K block c), so the term dmin * sum_j m_j * xd * bsum_j is one
+// fp32 MFMA pair per block (k = sub-block) that accumulates straight into
+// r: no int32 min accumulator, conversion or epilogue for it.
+template <int NB, int CH>
+__device__ __forceinline__ void q4w_mma_fm(const Q4W<CH> &w, const int8_t *aq, const float *ad, const float *amb,
+                                           float (&r)[4])
+{
+    const int lane = lane_id(), lr = lane & 15, q = lane >> 4;
+    // the min terms accumulate in the matrix core (rm), the scaled
+    // sub-block sums in the VALU (r): neither waits on the other
+    v4f rm = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint32_t y = w.hdr[c].y, z = w.hdr[c].z, x = w.hdr[c].w;
+        const uint32_t sc_lo = y & 0x3F3F3F3Fu, m_lo = z & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (x & 0x0F0F0F0Fu) | (((y >> 6) & 0x03030303u) << 4);
+        const uint32_t m_hi = ((x >> 4) & 0x0F0F0F0Fu) | (((z >> 6) & 0x03030303u) << 4);
+        const float d = h2f(w.hdr[c].x & 0xffff), ndmin = -h2f(w.hdr[c].x >> 16);
+        // min term: B[k = q][row] = -dmin * m_{4h + q}
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const float bm = ndmin * (float)(((hh ? m_hi : m_lo) >> (8 * q)) & 63);
+            rm = __builtin_amdgcn_mfma_f32_16x16x4f32(amb[(c * 2 + hh) * 64 + lane], bm, rm, 0, 0, 0);
+        }
+        int accs[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int hb = 0; hb < 2; hb++) {
+            v4i p[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int j = 4 * hb + jj;
+                const long a = *(const long *)(aq + lr * arow<NB>() + c * QK_K + 32 * j + 8 * q);
+                p[jj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, pack_nib(w.qs[c][j >> 1], j & 1), v4i{0, 0, 0, 0},
+                                                              0, 0, 0);
+            }
+            const uint32_t sw = hb ? sc_hi : sc_lo;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int sc = (int)((sw >> (8 * jj)) & 63);
+                accs[0] = __mul24(sc, p[jj][0]) + accs[0];
+                accs[1] = __mul24(sc, p[jj][1]) + accs[1];
+                accs[2] = __mul24(sc, p[jj][2]) + accs[2];
+                accs[3] = __mul24(sc, p[jj][3]) + accs[3];
+            }
+        }
+        const float4 xd = *(const float4 *)(ad + c * 16 + 4 * q);
+        r[0] += (d * xd.x) * (float)accs[0];
+        r[1] += (d * xd.y) * (float)accs[1];
+        r[2] += (d * xd.z) * (float)accs[2];
+        r[3] += (d * xd.w) * (float)accs[3];
+    }
+    r[0] += rm[0];
+    r[1] += rm[1];
+    r[2] += rm[2];
+    r[3] += rm[3];
+}
+
 // ------------------------------------------------------- Q6_K x Q8_K tile --
 // Same contract for Q6_K rows; one MFMA per 16-wide group, whose 16 values
 // sit in lanes q = 0, 1 (k 0..15); lanes q = 2, 3 carry zero weights.  For
@@ -504,7 +563,7 @@ constexpr int GR_ROWS = 32;
 // and each wave's token reads batch into one LDS round trip.
 template <int KH>
 __device__ __forceinline__ void stage_dma(const int *tok, int nbe, int kb0, const int8_t *xq, const float *xd,
-                                          int8_t *aq, float *ad)
+                                          const float *xmb, int8_t *aq, float *ad, float *amb)
 {
     const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
     const size_t xrow = (size_t)nbe * QK_K;
@@ -536,6 +595,16 @@ __device__ __forceinline__ void stage_dma(const int *tok, int nbe, int kb0, cons
             __builtin_amdgcn_global_load_lds((const QMAG_GLOBAL void *)(xd + (size_t)tok[p] * nbe + kb0 + c),
                                              (__attribute__((address_space(3))) void *)(ad + wv * 64), 4, 0, 0);
     }
+    // min-term operands, amb[(c*2 + h)*64 + 16*k + p] = xmb of pair p,
+    // block c, sub-block 4h + k: one 256-byte DMA per (block, half), each
+    // lane gathering its pair's value
+#pragma unroll
+    for (int i = wv; i < 2 * KH; i += 4) {
+        const int c = i >> 1, hh = i & 1;
+        __builtin_amdgcn_global_load_lds(
+            (const QMAG_GLOBAL void *)(xmb + (size_t)tok[lane & 15] * (nbe * 8) + (kb0 + c) * 8 + 4 * hh + (lane >> 4)),
+            (__attribute__((address_space(3))) void *)(amb + i * 64), 4, 0, 0);
+    }
 }
 
 template <int NBE>
@@ -543,7 +612,8 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
     const uint8_t *__restrict__ gate_exps, const uint8_t *__restrict__ up_exps,
     const uint8_t *__restrict__ gate_sh, const uint8_t *__restrict__ up_sh, int E, int S, int F,
     const int4 *__restrict__ chunk, const int *__restrict__ perm,
-    const int8_t *__restrict__ xq, const float *__restrict__ xd, float *__restrict__ h)
+    const int8_t *__restrict__ xq, const float *__restrict__ xd, const float *__restrict__ xmb,
+    float *__restrict__ h)
 {
     constexpr int KH = NBE < 8 ? NBE : 8;      // super-blocks held per pass
     constexpr int NPASS = NBE / KH;
@@ -551,6 +621,7 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
     // that reading one need not wait for the DMA into the other
     __shared__ __align__(16) int8_t s_aq0[PB * arow<KH>()], s_aq1[PB * arow<KH>()];
     __shared__ __align__(16) float s_ad0[KH * PB], s_ad1[KH * PB];
+    __shared__ __align__(16) float s_mb0[KH * 128], s_mb1[KH * 128];
     __shared__ int s_pair[MC], s_tok[MC];
     const int rchunks = F / GR_ROWS;
     const int u = (int)blockIdx.x / rchunks, rc = (int)blockIdx.x % rchunks;
@@ -593,7 +664,7 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) {
         if (ps > 0) q4w_load(w, wrow, ps * KH);
-        stage_dma<KH>(s_tok, NBE, ps * KH, xq, xd, s_aq0, s_ad0);
+        stage_dma<KH>(s_tok, NBE, ps * KH, xq, xd, xmb, s_aq0, s_ad0, s_mb0);
 #pragma unroll
         for (int m = 0; m < MC / PB; m++) {
             if (m < mtn) {                     // workgroup-uniform
@@ -601,13 +672,14 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
                 // then for every wave) and tile m-1's buffer is free
                 __syncthreads();
                 if (m + 1 < mtn)
-                    stage_dma<KH>(s_tok + PB * (m + 1), NBE, ps * KH, xq, xd, (m & 1) ? s_aq0 : s_aq1,
-                                  (m & 1) ? s_ad0 : s_ad1);
+                    stage_dma<KH>(s_tok + PB * (m + 1), NBE, ps * KH, xq, xd, xmb, (m & 1) ? s_aq0 : s_aq1,
+                                  (m & 1) ? s_ad0 : s_ad1, (m & 1) ? s_mb0 : s_mb1);
                 // the weight registers are opaque to the compiler from here,
                 // so it derives the MFMA operands anew per tile instead of
                 // keeping all of them (twice the registers) live across tiles
                 q4w_opaque(w);
-                q4w_mma<KH, KH>(w, 0, (m & 1) ? s_aq1 : s_aq0, (m & 1) ? s_ad1 : s_ad0, r[m]);
+                q4w_mma_fm<KH, KH>(w, (m & 1) ? s_aq1 : s_aq0, (m & 1) ? s_ad1 : s_ad0, (m & 1) ? s_mb1 : s_mb0,
+                                   r[m]);
             }
         }
         __syncthreads();                       // the buffers are free for the next pass / the hand-off
@@ -798,11 +870,11 @@ int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *lo
 
 template <int NBE>
 static void launch_gu(const qmag_moe_layer *L, int S, int max_chunks, const int4 *chunk,
-                      const int *perm, const int8_t *xq, const float *xd, float *h, hipStream_t s)
+                      const int *perm, const int8_t *xq, const float *xd, const float *xmb, float *h, hipStream_t s)
 {
     hipLaunchKernelGGL(gateup_rows_kernel<NBE>, dim3(max_chunks * (L->n_ff / GR_ROWS)), dim3(256), 0, s,
                        (const uint8_t *)L->gate_exps, (const uint8_t *)L->up_exps, (const uint8_t *)L->gate_shexp,
-                       (const uint8_t *)L->up_shexp, L->n_expert, S, L->n_ff, chunk, perm, xq, xd, h);
+                       (const uint8_t *)L->up_shexp, L->n_expert, S, L->n_ff, chunk, perm, xq, xd, xmb, h);
 }
 
 template <int NBF>
@@ -815,7 +887,7 @@ static void launch_dn(const qmag_moe_layer *L, int max_chunks, const int4 *chunk
 }
 
 int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, const float *gs,
-                const int8_t *xq, const float *xd, const int16_t *xs, float *h, int8_t *hq, float *hd,
+                const int8_t *xq, const float *xd, const float *xmb, float *h, int8_t *hq, float *hd,
                 int16_t *hs, const float *resid, float *out, hipStream_t s)
 {
     const int N = L->n_embd, F = L->n_ff, E = L->n_expert, K = L->n_used, S = K + 1;
@@ -838,11 +910,11 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
     prof_end(PROF_GROUP, s);
     prof_begin(PROF_GATEUP, s);
     switch (N / QK_K) {
-    case 1: launch_gu<1>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
-    case 2: launch_gu<2>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
-    case 4: launch_gu<4>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
-    case 8: launch_gu<8>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
-    default: launch_gu<16>(L, S, max_chunks, chunk, perm, xq, xd, h, s); break;
+    case 1: launch_gu<1>(L, S, max_chunks, chunk, perm, xq, xd, xmb, h, s); break;
+    case 2: launch_gu<2>(L, S, max_chunks, chunk, perm, xq, xd, xmb, h, s); break;
+    case 4: launch_gu<4>(L, S, max_chunks, chunk, perm, xq, xd, xmb, h, s); break;
+    case 8: launch_gu<8>(L, S, max_chunks, chunk, perm, xq, xd, xmb, h, s); break;
+    default: launch_gu<16>(L, S, max_chunks, chunk, perm, xq, xd, xmb, h, s); break;
     }
     prof_end(PROF_GATEUP, s);
     prof_begin(PROF_HQUANT, s);
