@@ -117,9 +117,9 @@ int qmag_prof_read(int kernel_id, long *count, double *total_ms);
 #define QMAG_OPT_COOP 3
 /* QMAG_OPT_GROUPED (default 1): qmag_moe_ffn_dev with T >= 8 tokens (the
    prefill form) runs the grouped expert GEMM: (token, slot) pairs bucketed
-   by expert, gate/up and down as int8 MFMA tiles of 16 pairs, each expert's
-   weights read once per 16 pairs; 0 selects the per-token launch sequence
-   (same results within the fp32 tolerance). */
+   by expert into chunks of up to 64, gate/up and down as int8 MFMA tiles of
+   16 pairs, each expert's weights read once per chunk; 0 selects the
+   per-token launch sequence (same results within the fp32 tolerance). */
 #define QMAG_OPT_GROUPED 4
 int qmag_set_option(int option, int value);
 int qmag_trace_read(void *dst, size_t bytes);
