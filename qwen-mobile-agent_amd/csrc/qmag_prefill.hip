@@ -5,16 +5,16 @@
 //   topk_kernel          (qmag_moe.hip) softmax/top-k, Q8_K(x), shared gate
 //   group_kernel         (token, slot) pairs bucketed by expert; the shared
 //                        expert is bucket E with one pair per token
-//   gateup_chunk_kernel  h = silu(x.G) * (x.U) per pair: chunks of up to 64
-//                        pairs of one expert x 64 gate and 64 up rows, one
-//                        v_mfma_i32_16x16x32_i8 per 16 pairs x 16 rows x
-//                        32-wide Q4_K sub-block with its 6-bit scale applied
-//                        to the int32 result, and one more against the
-//                        sub-block's min broadcast over its 32 k (the min
-//                        term, summed in the matrix core over the block)
+//   gateup_rows_kernel   h = silu(x.G) * (x.U) per pair: chunks of up to 64
+//                        pairs of one expert x 32 rows of h, the weight rows
+//                        resident in registers; one v_mfma_i32_16x16x32_i8
+//                        per 16 pairs x 16 rows x 32-wide Q4_K sub-block with
+//                        its 6-bit scale applied to the int32 result, the min
+//                        term on the fp32 MFMA
 //   q8k_quant_kernel     Q8_K(h) per pair
-//   down_grouped_kernel  y[pair] = Q8_K(h) . D^T: Q6_K per 16-wide group (the
-//                        MFMA's other 16 k are zero) or Q4_K per sub-block
+//   down_rows_kernel     y[pair] = Q8_K(h) . D^T per chunk x 64 rows: Q6_K
+//                        per 16-wide group (the MFMA's other 16 k are zero)
+//                        or Q4_K per sub-block
 //   combine_kernel       out[t] = sum_k w_k y[t,k] + gs y[t,shared] in the
 //                        reference order (nn.c:614-629), plus an optional
 //                        residual
@@ -28,10 +28,9 @@
 // fp32 epilogue (scale * xd * integer sum) is associated differently from
 // the reference's per-sub-block fp32 terms, well inside 1e-4 of max|y|.
 //
-// Every expert's gate/up weights are read once per 64-pair chunk and its
-// down weights once per 16-pair block (the shared expert's by every chunk
-// or block of tokens); the pair buffers (h: T*S*F fp32, y: T*S*N fp32) stay
-// in HBM between kernels.
+// Every expert's weights are read once per 64-pair chunk (the shared
+// expert's by every chunk of 64 tokens); the pair buffers (h: T*S*F fp32,
+// y: T*S*N fp32) stay in HBM between kernels.
 #include "qmag_internal.h"
 
 namespace qmag {
@@ -94,8 +93,7 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
 }
 
 // ---------------------------------------------------------------- group --
-// grp layout: cnt[E+1], off[E+2], tbo[E+2] (16-pair blocks per bucket,
-// prefix); blk[b] = the bucket of global 16-pair block b; chunk[c] = {bucket
+// grp layout: cnt[E+1], off[E+2]; chunk[c] = {bucket
 // (-1 past the last chunk), pairs, offset of its first pair in perm, 0}, one
 // int4 per MC-pair chunk, so a workgroup learns all it needs from one load;
 // perm[T*S] (pair ids = t*S + slot, bucketed by expert).  Positions
@@ -108,11 +106,11 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
 constexpr int MC = 64;            // pairs per chunk of the chunked GEMMs (4 MFMA tiles)
 
 __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel, int T, int K, int E,
-                                                     int *__restrict__ grp, int *__restrict__ blk,
+                                                     int *__restrict__ grp,
                                                      int4 *__restrict__ chunk, int max_chunks,
                                                      int *__restrict__ perm)
 {
-    __shared__ int s_cnt[257], s_off[258], s_fill[257], s_inc[257], s_binc[257], s_finc[257];
+    __shared__ int s_cnt[257], s_off[258], s_fill[257], s_inc[257], s_finc[257];
     __shared__ int s_bin[MC], s_binf[MC];     // partial chunks by MC - size
     __shared__ int s_nch;
     const int tid = (int)threadIdx.x, S = K + 1;
@@ -130,28 +128,24 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
     for (int p = tid; p < T * K; p += 1024) atomicAdd(&s_cnt[expert(p)], 1);
     if (tid == 0) s_cnt[E] = T;      // shared expert: every token
     __syncthreads();
-    // inclusive prefix sums of the pair counts, the 16-pair block counts and
-    // the full-chunk counts over the E + 1 buckets (Hillis-Steele in LDS, 9
+    // inclusive prefix sums of the pair counts and the full-chunk counts over the E + 1 buckets (Hillis-Steele in LDS, 9
     // steps); the partial chunks are counted per size
     if (tid <= E) {
         const int c = s_cnt[tid];
         s_inc[tid] = c;
-        s_binc[tid] = (c + PB - 1) / PB;
         s_finc[tid] = c / MC;
         if (c % MC) atomicAdd(&s_bin[MC - c % MC], 1);
     }
     __syncthreads();
     for (int d = 1; d <= 256; d <<= 1) {
-        int a = 0, b = 0, m = 0;
+        int a = 0, m = 0;
         if (tid <= E && tid >= d) {
             a = s_inc[tid - d];
-            b = s_binc[tid - d];
             m = s_finc[tid - d];
         }
         __syncthreads();
         if (tid <= E && tid >= d) {
             s_inc[tid] += a;
-            s_binc[tid] += b;
             s_finc[tid] += m;
         }
         __syncthreads();
@@ -171,24 +165,18 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
     }
     __syncthreads();
     if (tid <= E) {
-        int *cnt = grp, *off = grp + (E + 1), *tbo = off + (E + 2);
+        int *cnt = grp, *off = grp + (E + 1);
         const int c = s_cnt[tid];
         s_off[tid] = s_inc[tid] - c;
         cnt[tid] = c;
         off[tid] = s_inc[tid] - c;
-        const int nb = (c + PB - 1) / PB, b0 = s_binc[tid] - nb;
-        tbo[tid] = b0;
-        for (int i = 0; i < nb; i++) blk[b0 + i] = tid;
         const int nf = c / MC, f0 = s_finc[tid] - nf, o = s_inc[tid] - c;
         for (int i = 0; i < nf; i++) chunk[f0 + i] = make_int4(tid, MC, o + i * MC, 0);
         if (c % MC) {
             const int bin = MC - c % MC;
             chunk[s_finc[E] + s_bin[bin] + atomicAdd(&s_binf[bin], 1)] = make_int4(tid, c % MC, o + nf * MC, 0);
         }
-        if (tid == E) {
-            off[E + 1] = s_inc[E];
-            tbo[E + 1] = s_binc[E];
-        }
+        if (tid == E) off[E + 1] = s_inc[E];
     }
     __syncthreads();
     for (int p = tid; p < T * K; p += 1024) {
@@ -411,41 +399,6 @@ __device__ __forceinline__ void q6w_load(Q6W<NB> &w, const uint8_t *wrow)
     }
 }
 
-template <int NB>
-__device__ __forceinline__ void q6w_mma(const Q6W<NB> &w, const int8_t *aq, const float *ad, float (&r)[4])
-{
-    const int lane = lane_id(), lr = lane & 15, q = lane >> 4, qq = q & 1;
-#pragma unroll
-    for (int ib = 0; ib < NB; ib++) {
-        int acc[4] = {0, 0, 0, 0};
-        const uint32_t scw[4] = {w.sc16[ib].x, w.sc16[ib].y, w.sc16[ib].z, w.sc16[ib].w};
-#pragma unroll
-        for (int gg = 0; gg < 16; gg++) {
-            // group gg = 8n + 2Q + hl: elements 128n + 32Q + 16hl + 0..15
-            const int n = gg >> 3, Q = (gg >> 1) & 3, hl = gg & 1;
-            const uint2 l8 = w.ql[ib][n][hl][Q & 1], h8 = w.qh[ib][n][hl];
-            const uint32_t lo0 = Q < 2 ? l8.x & 0x0F0F0F0Fu : (l8.x >> 4) & 0x0F0F0F0Fu;
-            const uint32_t lo1 = Q < 2 ? l8.y & 0x0F0F0F0Fu : (l8.y >> 4) & 0x0F0F0F0Fu;
-            const uint32_t hb0 = ((h8.x >> (2 * Q)) & 0x03030303u) << 4;
-            const uint32_t hb1 = ((h8.y >> (2 * Q)) & 0x03030303u) << 4;
-            const long b = q < 2 ? (long)(((unsigned long long)q6_center(lo1 | hb1) << 32) | q6_center(lo0 | hb0)) : 0;
-            const long a = *(const long *)(aq + lr * arow<NB>() + ib * QK_K + 128 * n + 32 * Q + 16 * hl + 8 * qq);
-            const v4i p = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
-            const int sc = (int)(int8_t)((scw[gg >> 2] >> (8 * (gg & 3))) & 255);
-            acc[0] = __mul24(sc, p[0]) + acc[0];
-            acc[1] = __mul24(sc, p[1]) + acc[1];
-            acc[2] = __mul24(sc, p[2]) + acc[2];
-            acc[3] = __mul24(sc, p[3]) + acc[3];
-        }
-        const float d = h2f(w.dbits[ib]);
-        const float4 xd = *(const float4 *)(ad + ib * 16 + 4 * q);
-        r[0] += d * xd.x * (float)acc[0];
-        r[1] += d * xd.y * (float)acc[1];
-        r[2] += d * xd.z * (float)acc[2];
-        r[3] += d * xd.w * (float)acc[3];
-    }
-}
-
 // The same rows with every group's MFMA operand built once (centred 6-bit
 // values, lanes q = 2, 3 zero): a workgroup that runs several M tiles
 // against the same rows unpacks them once instead of per tile.
@@ -519,28 +472,6 @@ __device__ __forceinline__ void q6b_mma(const Q6B<NB> &u, const int8_t *aq, cons
         r[1] += d * xd.y * (float)acc[1];
         r[2] += d * xd.z * (float)acc[2];
         r[3] += d * xd.w * (float)acc[3];
-    }
-}
-
-// Stage the Q8_K rows of the block's pairs into LDS (zeros for missing
-// pairs).  src rows are indexed by `row_of(pair)`; NB blocks of 256 each.
-// (The Q4_K min term is taken by the matrix core from the staged xq, so the
-// Q8_K group sums are not needed here.)
-template <int NB, typename RowOf>
-__device__ __forceinline__ void stage_q8k(const int *s_pair, RowOf row_of, const int8_t *xq, const float *xd,
-                                          int8_t *aq, float *ad)
-{
-    const int tid = (int)threadIdx.x;
-    constexpr int L = NB * QK_K;
-    for (int c = tid; c < PB * L / 16; c += 256) {
-        const int tok = c / (L / 16), part = c % (L / 16);
-        const int pr = s_pair[tok];
-        const uint4 v = pr >= 0 ? *(const uint4 *)(xq + (size_t)row_of(pr) * L + part * 16) : make_uint4(0, 0, 0, 0);
-        *(uint4 *)(aq + tok * arow<NB>() + part * 16) = v;
-    }
-    for (int c = tid; c < NB * PB; c += 256) {
-        const int ib = c / PB, tok = c % PB, pr = s_pair[tok];
-        ad[ib * PB + tok] = pr >= 0 ? xd[(size_t)row_of(pr) * NB + ib] : 0.0f;
     }
 }
 
@@ -718,22 +649,6 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
 // DMA, and y[pair][row] = row . Q8_K(h[pair]) runs M tile by M tile.
 constexpr int DN_ROWS = 64;
 
-template <int NB>
-__device__ __forceinline__ void q6w_opaque(Q6W<NB> &w)
-{
-#pragma unroll
-    for (int ib = 0; ib < NB; ib++) {
-        asm volatile("" : "+v"(w.sc16[ib].x), "+v"(w.sc16[ib].y), "+v"(w.sc16[ib].z), "+v"(w.sc16[ib].w),
-                     "+v"(w.dbits[ib]));
-#pragma unroll
-        for (int n = 0; n < 2; n++)
-#pragma unroll
-            for (int hl = 0; hl < 2; hl++)
-                asm volatile("" : "+v"(w.ql[ib][n][hl][0].x), "+v"(w.ql[ib][n][hl][0].y), "+v"(w.ql[ib][n][hl][1].x),
-                             "+v"(w.ql[ib][n][hl][1].y), "+v"(w.qh[ib][n][hl].x), "+v"(w.qh[ib][n][hl].y));
-    }
-}
-
 // stage rows[0 .. 16*mtn) of Q8_K(h) (NB super-blocks each) into
 // aq[p][arow<NB>()] and their scales into ad[p / 16][block][p % 16]: one
 // 256-byte DMA per (pair, block), one dword per lane; every pair slot has a
@@ -892,21 +807,20 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
 {
     const int N = L->n_embd, F = L->n_ff, E = L->n_expert, K = L->n_used, S = K + 1;
     int st;
-    // upper bounds of the 16-pair blocks and the MC-pair chunks: sum
-    // ceil(n_e / 16) <= T*K/16 + E, plus the shared bucket
-    const int max_blocks = (T * K + PB - 1) / PB + E + (T + PB - 1) / PB;
+    // upper bound of the MC-pair chunks: sum ceil(n_e / MC) <= T*K/MC + E,
+    // plus the shared bucket
     const int max_chunks = (T * K + MC - 1) / MC + E + (T + MC - 1) / MC;
     // int4 chunk descriptors first (16-byte aligned), then the int tables
     int4 *chunk = (int4 *)workspace(WS_GRP, sizeof(int4) * (size_t)max_chunks +
-                                                sizeof(int) * ((size_t)4 * (E + 2) + max_blocks + (size_t)T * S),
+                                                sizeof(int) * ((size_t)2 * (E + 2) + (size_t)T * S),
                                     &st);
     if (st) return st;
-    int *grp = (int *)(chunk + max_chunks), *blk = grp + 4 * (E + 2), *perm = blk + max_blocks;
+    int *grp = (int *)(chunk + max_chunks), *perm = grp + 2 * (E + 2);
     float *y = (float *)workspace(WS_Y, sizeof(float) * (size_t)T * S * N, &st);
     if (st) return st;
 
     prof_begin(PROF_GROUP, s);
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, sel, T, K, E, grp, blk, chunk, max_chunks, perm);
+    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(1024), 0, s, sel, T, K, E, grp, chunk, max_chunks, perm);
     prof_end(PROF_GROUP, s);
     prof_begin(PROF_GATEUP, s);
     switch (N / QK_K) {
