@@ -307,39 +307,57 @@ __device__ __forceinline__ float d_dot(const DRaw<TD> &d, const uint32_t *hq, co
 // picks (the sum taken in pick order).
 __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, float &my_w)
 {
+    // top-K on the logits themselves (softmax is monotonic, so the selection
+    // is the reference's), then w_k = exp(l_k - l_max) / sum over the K
+    // selected, which is p_k / sum_sel p of nn.c:522-536 with the full
+    // softmax sum cancelled.  Each lane sorts its four candidates (experts
+    // lane + 64j) once; a round is then one wave max over the lane heads,
+    // one ballot for the winning lane, and a shift of that lane's list.
     const int lane = lane_id();
-    float p[4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; j++) mx = fmaxf(mx, lg[j]);
-    mx = group_max<64>(mx);
-    float se = 0.0f;
+    float v[4];
+    int id[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        p[j] = lane + 64 * j < E ? expf(lg[j] - mx) : 0.0f;
-        se += p[j];
+        v[j] = lane + 64 * j < E ? lg[j] : -INFINITY;
+        id[j] = lane + 64 * j;
     }
-    se = group_sum<64>(se);
-#pragma unroll
-    for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < E ? p[j] / se : -1.0f;
-    float ws = 0.0f;
+    auto cswap = [&](int i, int j) {           // descending; an equal pair keeps its order
+        const bool sw = v[j] > v[i];
+        const float vi = v[i], vj = v[j];
+        const int ii = id[i], ij = id[j];
+        v[i] = sw ? vj : vi;
+        v[j] = sw ? vi : vj;
+        id[i] = sw ? ij : ii;
+        id[j] = sw ? ii : ij;
+    };
+    cswap(0, 1);
+    cswap(2, 3);
+    cswap(0, 2);
+    cswap(1, 3);
+    cswap(1, 2);
+    float my_l = -INFINITY, l0 = 0.0f;
     for (int k = 0; k < K; k++) {
-        const float m = group_max<64>(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])));
-        const unsigned long long b0 = __ballot(p[0] == m), b1 = __ballot(p[1] == m), b2 = __ballot(p[2] == m),
-                                 b3 = __ballot(p[3] == m);
-        // NaN probabilities equal nothing: fall back to expert 0, in range
-        const int e = b0 ? __builtin_ctzll(b0) : b1 ? 64 + __builtin_ctzll(b1)
-                    : b2 ? 128 + __builtin_ctzll(b2) : b3 ? 192 + __builtin_ctzll(b3) : 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (lane + 64 * j == e) p[j] = -1.0f;
+        const float m = group_max<64>(v[0]);
+        const unsigned long long bal = __ballot(v[0] == m);
+        // a NaN maximum equals nothing: fall back to lane 0's head, in range
+        const int win = bal ? __builtin_ctzll(bal) : 0;
+        const int e = __builtin_amdgcn_readlane(id[0], win);
+        const bool me = lane == win;
+        v[0] = me ? v[1] : v[0];
+        v[1] = me ? v[2] : v[1];
+        v[2] = me ? v[3] : v[2];
+        v[3] = me ? -INFINITY : v[3];
+        id[0] = me ? id[1] : id[0];
+        id[1] = me ? id[2] : id[1];
+        id[2] = me ? id[3] : id[2];
         if (lane == k) {
             my_sel = e;
-            my_w = m;
+            my_l = m;
         }
-        ws += m;
+        if (k == 0) l0 = m;
     }
-    my_w = my_w / ws;
+    const float ex = lane < K ? expf(my_l - l0) : 0.0f;
+    my_w = ex / group_sum<8>(ex);
 }
 
 template <int TD>
