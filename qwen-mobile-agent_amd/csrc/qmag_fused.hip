@@ -782,6 +782,14 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
 static qmag_moe_layer *g_dev_layers = nullptr;
 static qmag_moe_layer g_host_copy[256];
 static int g_host_n = 0;
+// one-layer calls (the moe_ffn seam, one layer per call, rotating over a
+// model's layers) keep every distinct descriptor resident in its own slot:
+// uploaded the first time it is seen, found by a hash of its bytes after
+constexpr int ONE_SLOTS = 256, ONE_HASH = 1024;
+static qmag_moe_layer *g_dev_one = nullptr;
+static qmag_moe_layer g_one_host[ONE_SLOTS];
+static int g_one_n = 0;
+static short g_one_table[ONE_HASH];         // slot + 1, 0 = empty (linear probing)
 static fused::Tagged *g_tagged = nullptr;
 static int *g_abort = nullptr;
 static unsigned g_epoch = 0;        // launches since the tagged buffers were last zeroed
@@ -836,10 +844,44 @@ int fused_status()
     return QMAG_OK;
 }
 
-static int fused_prepare(const qmag_moe_layer *L, int n_layer, hipStream_t s)
+static uint32_t layer_hash(const qmag_moe_layer *L)
+{
+    const unsigned char *p = (const unsigned char *)L;
+    uint32_t h = 2166136261u;                       // FNV-1a over the descriptor bytes
+    for (size_t i = 0; i < sizeof(qmag_moe_layer); i++) h = (h ^ p[i]) * 16777619u;
+    return h;
+}
+
+// device copy of a one-layer descriptor, uploading it on first sight
+static int one_layer_slot(const qmag_moe_layer *L, hipStream_t s, const qmag_moe_layer **dl)
+{
+    uint32_t i = layer_hash(L) % ONE_HASH;
+    for (; g_one_table[i]; i = (i + 1) % ONE_HASH) {
+        const int slot = g_one_table[i] - 1;
+        if (memcmp(&g_one_host[slot], L, sizeof(qmag_moe_layer)) == 0) {
+            *dl = g_dev_one + slot;
+            return QMAG_OK;
+        }
+    }
+    if (g_one_n == ONE_SLOTS) {                    // full: start over (launches in flight may read slots)
+        QMAG_HIP(hipStreamSynchronize(s));
+        g_one_n = 0;
+        memset(g_one_table, 0, sizeof(g_one_table));
+        for (i = layer_hash(L) % ONE_HASH; g_one_table[i]; i = (i + 1) % ONE_HASH) {}
+    }
+    const int slot = g_one_n++;
+    QMAG_HIP(hipMemcpy(g_dev_one + slot, L, sizeof(qmag_moe_layer), hipMemcpyHostToDevice));
+    g_one_host[slot] = *L;
+    g_one_table[i] = (short)(slot + 1);
+    *dl = g_dev_one + slot;
+    return QMAG_OK;
+}
+
+static int fused_prepare(const qmag_moe_layer *L, int n_layer, hipStream_t s, const qmag_moe_layer **dl)
 {
     if (!g_dev_layers) {
         QMAG_HIP(hipMalloc(&g_dev_layers, sizeof(qmag_moe_layer) * 256));
+        QMAG_HIP(hipMalloc(&g_dev_one, sizeof(qmag_moe_layer) * ONE_SLOTS));
         QMAG_HIP(hipMalloc(&g_tagged, sizeof(fused::Tagged)));
         QMAG_HIP(hipMalloc(&g_abort, 128));
         QMAG_HIP(hipMalloc(&g_logits, sizeof(float) * 256));
@@ -850,11 +892,17 @@ static int fused_prepare(const qmag_moe_layer *L, int n_layer, hipStream_t s)
         int st = rearm();
         if (st) return st;
     }
-    if (g_host_n != n_layer || memcmp(g_host_copy, L, sizeof(qmag_moe_layer) * (size_t)n_layer) != 0) {
-        QMAG_HIP(hipStreamSynchronize(s));
-        QMAG_HIP(hipMemcpy(g_dev_layers, L, sizeof(qmag_moe_layer) * (size_t)n_layer, hipMemcpyHostToDevice));
-        memcpy(g_host_copy, L, sizeof(qmag_moe_layer) * (size_t)n_layer);
-        g_host_n = n_layer;
+    if (n_layer == 1) {
+        int st = one_layer_slot(L, s, dl);
+        if (st) return st;
+    } else {
+        if (g_host_n != n_layer || memcmp(g_host_copy, L, sizeof(qmag_moe_layer) * (size_t)n_layer) != 0) {
+            QMAG_HIP(hipStreamSynchronize(s));
+            QMAG_HIP(hipMemcpy(g_dev_layers, L, sizeof(qmag_moe_layer) * (size_t)n_layer, hipMemcpyHostToDevice));
+            memcpy(g_host_copy, L, sizeof(qmag_moe_layer) * (size_t)n_layer);
+            g_host_n = n_layer;
+        }
+        *dl = g_dev_layers;
     }
     if (g_epoch >= (1u << 24)) {           // tags would wrap: zero the buffers, restart
         int st = rearm();
@@ -882,9 +930,9 @@ static int fused_prepare(const qmag_moe_layer *L, int n_layer, hipStream_t s)
 int fused_launch(const qmag_moe_layer *L, int n_layer, float *x, float *out, hipStream_t s)
 {
     if (out && n_layer != 1) return fail(QMAG_ERR_ARG, "fused: out mode needs exactly one layer");
-    int st = fused_prepare(L, n_layer, s);
+    const qmag_moe_layer *dl = nullptr;
+    int st = fused_prepare(L, n_layer, s, &dl);
     if (st) return st;
-    const qmag_moe_layer *dl = g_dev_layers;
     unsigned epoch = g_epoch;
     unsigned long long *trace = option(QMAG_OPT_TRACE) ? g_trace : nullptr;
     void *args[] = {(void *)&dl,      (void *)&n_layer, (void *)&x,     (void *)&out,
