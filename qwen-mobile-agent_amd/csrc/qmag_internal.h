@@ -63,6 +63,8 @@ int launch_q8k_quant(const float *x, int nblocks, int8_t *xq, float *xd, int16_t
                      hipStream_t s);
 int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
                   int n_in, int n_out, int T, int wtype, float *out, hipStream_t s);
+// T = 1 with x in f32: the matvec quantises x to Q8_K itself (bit-identical)
+int launch_matvec_x(const float *x, const void *W, int n_in, int n_out, int wtype, float *out, hipStream_t s);
 int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const float *resid,
             hipStream_t s);
 int moe_check_layer(const qmag_moe_layer *L);

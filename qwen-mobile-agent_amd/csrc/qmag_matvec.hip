@@ -96,12 +96,18 @@ struct RowTask<QMAG_TYPE_Q6_K> {
     }
 };
 
-template <int WT, int NB, bool ONE_TOKEN>
+// ONE_TOKEN: T = 1, the activation operand is loaded once per lane.  XF
+// (with ONE_TOKEN): the kernel takes x itself and every workgroup computes
+// its Q8_K into LDS with the same per-block routine as q8k_quant_kernel
+// (bit-identical), after its first weight rows are requested -- one launch
+// per matvec instead of two.
+template <int WT, int NB, bool ONE_TOKEN, bool XF = false>
 __global__ __launch_bounds__(256) void matvec_kernel(const uint8_t *__restrict__ W,
                                                      const int8_t *__restrict__ xq,
                                                      const float *__restrict__ xd,
                                                      const int16_t *__restrict__ xsum,
-                                                     float *__restrict__ out, int n_out, int T)
+                                                     float *__restrict__ out, int n_out, int T,
+                                                     const float *__restrict__ xf = nullptr)
 {
     using RT = RowTask<WT>;
     constexpr int TPR = 4 * NB;                 // tasks per row
@@ -118,14 +124,8 @@ __global__ __launch_bounds__(256) void matvec_kernel(const uint8_t *__restrict__
     const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int nwave = (int)((gridDim.x * blockDim.x) >> 6);
 
-    typename RT::Act act[TPL];
-    if constexpr (ONE_TOKEN) {
-#pragma unroll
-        for (int j = 0; j < TPL; j++) RT::load_act(act[j], xq, xd, xsum, (sub + LPR * j) >> 2, q);
-    }
-
-    for (int base = wave * RPW * U; base < n_out; base += nwave * RPW * U) {
-        typename RT::Raw raw[U][TPL];
+    typename RT::Raw raw[U][TPL];
+    auto load_rows = [&](int base) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int row = base + u * RPW + rw;
@@ -137,6 +137,31 @@ __global__ __launch_bounds__(256) void matvec_kernel(const uint8_t *__restrict__
                     raw[u][j] = typename RT::Raw{};
             }
         }
+    };
+    const int base0 = wave * RPW * U;
+    typename RT::Act act[TPL];
+    if constexpr (XF) {
+        __shared__ __align__(16) int8_t s_xq[N_IN];
+        __shared__ float s_xd[NB];
+        __shared__ __align__(16) int16_t s_xs[N_IN / 16];
+        load_rows(base0);                       // the weights are in flight during the quantisation
+        const int wv = (int)(threadIdx.x >> 6);
+        for (int b = wv; b < NB; b += 4) {
+            const Q8Lane r = q8k_quant_lane(ldg4(xf + b * QK_K + 4 * lane));
+            ((uint32_t *)(s_xq + b * QK_K))[lane] = r.packed;
+            if (lane == 0) s_xd[b] = r.d;
+            if ((lane & 3) == 0) s_xs[b * 16 + (lane >> 2)] = (int16_t)r.gsum;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TPL; j++) RT::load_act(act[j], s_xq, s_xd, s_xs, (sub + LPR * j) >> 2, q);
+    } else if constexpr (ONE_TOKEN) {
+#pragma unroll
+        for (int j = 0; j < TPL; j++) RT::load_act(act[j], xq, xd, xsum, (sub + LPR * j) >> 2, q);
+    }
+
+    for (int base = base0; base < n_out; base += nwave * RPW * U) {
+        if (!XF || base != base0) load_rows(base);
         for (int t = 0; t < T; t++) {
             if constexpr (!ONE_TOKEN) {
 #pragma unroll
@@ -159,7 +184,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(const uint8_t *__restrict__
 
 template <int WT, int NB>
 static int launch_mv_nb(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
-                        int n_out, int T, float *out, hipStream_t s)
+                        int n_out, int T, float *out, hipStream_t s, const float *xf)
 {
     constexpr int TPR = 4 * NB;
     constexpr int LPR = TPR < 64 ? TPR : 64;
@@ -169,12 +194,15 @@ static int launch_mv_nb(const int8_t *xq, const float *xd, const int16_t *xsum, 
     const long waves = groups < cap ? groups : cap;
     const int wgs = (int)((waves + 3) / 4);
     prof_begin(PROF_MATVEC, s);
-    if (T == 1)
+    if (xf)
+        hipLaunchKernelGGL((matvec_kernel<WT, NB, true, true>), dim3(wgs), dim3(256), 0, s,
+                           (const uint8_t *)W, xq, xd, xsum, out, n_out, 1, xf);
+    else if (T == 1)
         hipLaunchKernelGGL((matvec_kernel<WT, NB, true>), dim3(wgs), dim3(256), 0, s,
-                           (const uint8_t *)W, xq, xd, xsum, out, n_out, T);
+                           (const uint8_t *)W, xq, xd, xsum, out, n_out, T, nullptr);
     else
         hipLaunchKernelGGL((matvec_kernel<WT, NB, false>), dim3(wgs), dim3(256), 0, s,
-                           (const uint8_t *)W, xq, xd, xsum, out, n_out, T);
+                           (const uint8_t *)W, xq, xd, xsum, out, n_out, T, nullptr);
     prof_end(PROF_MATVEC, s);
     QMAG_HIP(hipGetLastError());
     return QMAG_OK;
@@ -182,15 +210,15 @@ static int launch_mv_nb(const int8_t *xq, const float *xd, const int16_t *xsum, 
 
 template <int WT>
 static int launch_mv_t(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
-                       int n_in, int n_out, int T, float *out, hipStream_t s)
+                       int n_in, int n_out, int T, float *out, hipStream_t s, const float *xf)
 {
     switch (n_in / QK_K) {
-    case 1: return launch_mv_nb<WT, 1>(xq, xd, xsum, W, n_out, T, out, s);
-    case 2: return launch_mv_nb<WT, 2>(xq, xd, xsum, W, n_out, T, out, s);
-    case 4: return launch_mv_nb<WT, 4>(xq, xd, xsum, W, n_out, T, out, s);
-    case 8: return launch_mv_nb<WT, 8>(xq, xd, xsum, W, n_out, T, out, s);
-    case 16: return launch_mv_nb<WT, 16>(xq, xd, xsum, W, n_out, T, out, s);
-    case 32: return launch_mv_nb<WT, 32>(xq, xd, xsum, W, n_out, T, out, s);
+    case 1: return launch_mv_nb<WT, 1>(xq, xd, xsum, W, n_out, T, out, s, xf);
+    case 2: return launch_mv_nb<WT, 2>(xq, xd, xsum, W, n_out, T, out, s, xf);
+    case 4: return launch_mv_nb<WT, 4>(xq, xd, xsum, W, n_out, T, out, s, xf);
+    case 8: return launch_mv_nb<WT, 8>(xq, xd, xsum, W, n_out, T, out, s, xf);
+    case 16: return launch_mv_nb<WT, 16>(xq, xd, xsum, W, n_out, T, out, s, xf);
+    case 32: return launch_mv_nb<WT, 32>(xq, xd, xsum, W, n_out, T, out, s, xf);
     default: return fail(QMAG_ERR_ARG, "matvec: n_in=%d not in {256..8192} powers of two", n_in);
     }
 }
@@ -202,8 +230,19 @@ int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const 
         return fail(QMAG_ERR_ARG, "matvec: n_in=%d n_out=%d T=%d", n_in, n_out, T);
     if (!xq || !xd || !W || !out || (wtype == QMAG_TYPE_Q4_K && !xsum))
         return fail(QMAG_ERR_ARG, "matvec: null pointer");
-    if (wtype == QMAG_TYPE_Q4_K) return launch_mv_t<QMAG_TYPE_Q4_K>(xq, xd, xsum, W, n_in, n_out, T, out, s);
-    if (wtype == QMAG_TYPE_Q6_K) return launch_mv_t<QMAG_TYPE_Q6_K>(xq, xd, xsum, W, n_in, n_out, T, out, s);
+    if (wtype == QMAG_TYPE_Q4_K) return launch_mv_t<QMAG_TYPE_Q4_K>(xq, xd, xsum, W, n_in, n_out, T, out, s, nullptr);
+    if (wtype == QMAG_TYPE_Q6_K) return launch_mv_t<QMAG_TYPE_Q6_K>(xq, xd, xsum, W, n_in, n_out, T, out, s, nullptr);
+    return fail(QMAG_ERR_ARG, "matvec: unsupported wtype %d", wtype);
+}
+
+int launch_matvec_x(const float *x, const void *W, int n_in, int n_out, int wtype, float *out, hipStream_t s)
+{
+    if (n_in <= 0 || n_in % QK_K || n_out <= 0) return fail(QMAG_ERR_ARG, "matvec: n_in=%d n_out=%d", n_in, n_out);
+    if (!x || !W || !out) return fail(QMAG_ERR_ARG, "matvec: null pointer");
+    if (wtype == QMAG_TYPE_Q4_K)
+        return launch_mv_t<QMAG_TYPE_Q4_K>(nullptr, nullptr, nullptr, W, n_in, n_out, 1, out, s, x);
+    if (wtype == QMAG_TYPE_Q6_K)
+        return launch_mv_t<QMAG_TYPE_Q6_K>(nullptr, nullptr, nullptr, W, n_in, n_out, 1, out, s, x);
     return fail(QMAG_ERR_ARG, "matvec: unsupported wtype %d", wtype);
 }
 

@@ -336,6 +336,8 @@ int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, i
     int st = require_ready();
     if (st) return st;
     if (n_in <= 0 || n_in % QK_K || T <= 0) return fail(QMAG_ERR_ARG, "matmul: n_in=%d T=%d", n_in, T);
+    // one token: the matvec quantises x itself (one launch)
+    if (T == 1) return launch_matvec_x(x, W, n_in, n_out, wtype, out, g_ctx.stream);
     int8_t *xq = (int8_t *)workspace(WS_XQ, (size_t)T * n_in, &st);
     if (st) return st;
     float *xd = (float *)workspace(WS_XD, sizeof(float) * (size_t)T * (n_in / QK_K), &st);
