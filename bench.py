@@ -95,9 +95,9 @@ def matvec_bytes(n_in: int, n_out: int, wtype: int) -> int:
 
 
 def aux_matvec(name: str, n_in: int, n_out: int, wtype: int, copies: int, iters: int) -> dict:
-    """Configs C1/C2: the matmul seam (Q8_K of x, then the matvec) at T = 1,
-    rotating over `copies` distinct weight matrices so the working set
-    exceeds the 256 MB last-level cache."""
+    """Configs C1/C2: the matmul seam at T = 1 (one launch: the matvec
+    quantises x to Q8_K itself), rotating over `copies` distinct weight
+    matrices so the working set exceeds the 256 MB last-level cache."""
     rb = n_in // 256 * (144 if wtype == 12 else 210)
     Ws = [qmag.DBuf(rb * n_out) for _ in range(copies)]
     for i, w in enumerate(Ws):
