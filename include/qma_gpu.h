@@ -136,7 +136,8 @@ int qmag_q8k_quant_dev(const float *x, int n, int T, int8_t *xq, float *xd, int1
 int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum,
                         const void *W, int n_in, int n_out, int T, int wtype, float *out);
 
-/* matmul seam, nn.c:307-345: quantise each x[t] once, then the matvec. */
+/* matmul seam, nn.c:307-345: quantise each x[t] once, then the matvec (for
+   T = 1 a single launch: the matvec quantises x itself, bit-identically). */
 int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
                     float *out);
 
