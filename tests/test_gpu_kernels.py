@@ -120,6 +120,28 @@ def test_matvec_vs_oracle(qm, orc, wtype, n_in, n_out, T):
     assert max_rel_err(got, ref) < TOL
 
 
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("n_in,n_out", [(256, 33), (2048, 2048), (8192, 65)])
+def test_matmul_one_launch_equals_two_step(qm, orc, wtype, n_in, n_out):
+    """At T = 1 the matmul seam is one launch (the matvec quantises x in LDS
+    with the routine of the Q8_K kernel); its output must equal, bit for bit,
+    the two-step form: Q8_K kernel, then the matvec on the stored operand.
+    x carries exact .5 ties and a spike so the rounding paths are exercised."""
+    W = orc.quantize(orc.fill_normal(2000 + n_in + n_out, n_in * n_out, 0.0, 0.02), wtype)
+    x = orc.fill_normal(11 + n_in, n_in, 0.0, 1.0)
+    x[::97] = np.float32(2.5)
+    x[5] = np.float32(-9.0)
+    xb, xq, xd, xs = _q8_dev(qm, x, n_in, 1)
+    Wb = qm.DBuf.from_array(W)
+    one = qm.DBuf(4 * n_out)
+    two = qm.DBuf(4 * n_out)
+    qm.matmul_dev(xb, Wb, n_in, n_out, 1, wtype, one)
+    qm.matmul_q8k_dev(xq, xd, xs, Wb, n_in, n_out, 1, wtype, two)
+    a = one.download(np.float32)
+    b = two.download(np.float32)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_lm_head_shape_q6k(qm, orc):
     """C2 shape (151,936 x 2048, Q6_K) generated on the GPU; the full output
     vector is checked against the oracle run on the downloaded bytes."""
