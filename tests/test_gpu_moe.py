@@ -291,3 +291,31 @@ def test_moe_stack_qwen35moe_shape(qm, orc, decode_path):
     for t in range(2):
         ref = orc.moe_stack(hls, x[t * 2048:(t + 1) * 2048])
         assert max_rel_err(got[t], ref) < TOL
+
+
+def test_moe_layer_descriptor_reuse(qm):
+    """One-layer decode calls keep each distinct layer descriptor resident on
+    the device, found by content: alternating layers must give the same
+    bits as the first call on each, and a descriptor rewritten in place at
+    the same host address must be seen with its new contents."""
+    rls = [qm.ResidentLayer(seed=91, layer=l) for l in range(2)]
+    x = qm.DBuf.from_array(np.random.default_rng(5).standard_normal(2048).astype(np.float32))
+    outs = [qm.DBuf(4 * 2048) for _ in range(4)]
+
+    def run(desc, o):
+        qm.moe_ffn_dev(desc, x.ptr, o.ptr, 1)
+        qm.sync()
+        return o.download(np.float32).view(np.uint32).copy()
+
+    a0 = run(rls[0].c, outs[0])
+    a1 = run(rls[1].c, outs[1])
+    a2 = run(rls[0].c, outs[2])
+    assert np.array_equal(a0, a2)
+    assert not np.array_equal(a0, a1)
+    desc = type(rls[1].c).from_buffer_copy(rls[1].c)
+    assert np.array_equal(run(desc, outs[3]), a1)
+    for name, _ in type(desc)._fields_:
+        setattr(desc, name, getattr(rls[0].c, name))
+    assert np.array_equal(run(desc, outs[3]), a0)
+    for r in rls:
+        r.close()
