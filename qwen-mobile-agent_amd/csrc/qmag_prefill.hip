@@ -7,10 +7,10 @@
 //                        expert is bucket E with one pair per token
 //   gateup_rows_kernel   h = silu(x.G) * (x.U) per pair: chunks of up to 64
 //                        pairs of one expert x 32 rows of h, the weight rows
-//                        resident in registers; one v_mfma_i32_16x16x32_i8
-//                        per 16 pairs x 16 rows x 32-wide Q4_K sub-block with
-//                        its 6-bit scale applied to the int32 result, the min
-//                        term on the fp32 MFMA
+//                        resident in registers; the 6-bit sub-block scales
+//                        folded into the weight operand (sc = 8 sh + sl), two
+//                        v_mfma_i32_16x16x64_i8 chains per 16 pairs x 16 rows
+//                        x 64 k, the min term on the fp32 MFMA
 //   q8k_quant_kernel     Q8_K(h) per pair
 //   down_rows_kernel     y[pair] = Q8_K(h) . D^T per chunk x 64 rows: Q6_K
 //                        per 16-wide group (the MFMA's other 16 k are zero)
@@ -19,9 +19,12 @@
 //                        reference order (nn.c:614-629), plus an optional
 //                        residual
 //
-// Integer parity: each MFMA result is the exact int32 dot of one sub-block
-// (Q4_K) or group (Q6_K) -- the integer sums of src/q8k.c -- and the scale
-// products are accumulated exactly in int32 per super-block (with 24-bit
+// Integer parity: each MFMA result is an exact int32 sum -- of one
+// sub-block or group (the down path), or of a super-block with the
+// sub-block scales folded in (gate/up: sum_j sc_j P_j = sum(q sl) + 8
+// sum(q sh), every operand byte <= 105) -- the integer sums of src/q8k.c;
+// where the scale products are formed after the MFMA they are accumulated
+// exactly in int32 per super-block (with 24-bit
 // multiplies, exact here: |MFMA result| <= 32*15*128 < 2^17 and the
 // scales are 6- or 8-bit; v_mad_i32_i24 runs at the full VALU rate where a
 // 32-bit multiply takes four passes); only the
@@ -303,19 +306,33 @@ __device__ __forceinline__ void q4w_mma(const Q4W<CH> &w, int c0, const int8_t *
     }
 }
 
-// Same contract, with the min term taken from a precomputed operand:
+// The same product for one or two M tiles (NT) sharing the weight rows,
+// with the 6-bit sub-block scale folded into the weight operand instead of
+// applied to each result: sc = 8*sh + sl with sl, sh in 0..7, so q*sl and
+// q*sh (q <= 15) are int8 values <= 105, and
+//     sum_j sc_j P_j = sum_k a_k (q_k sl_j) + 8 sum_k a_k (q_k sh_j)
+// is two K = 64 MFMA chains over the block (two sub-blocks per MFMA: bytes
+// 0-7 of a lane's operands are its k of sub-block 2t, bytes 8-15 those of
+// 2t+1), exact in int32.  The scaled operands are built once per block (a
+// packed 16-bit multiply per 4 bytes: no byte overflows into the next) and
+// serve every tile; the per-result multiply-adds are gone.  The min term
+// dmin * sum_j m_j * xd * bsum_j takes a precomputed operand,
 // amb[(c*2 + h)*64 + 16*k + p] = xd_c(pair p) * (sum of sub-block 4h + k of
-// pair p's Q8_K block c), so the term dmin * sum_j m_j * xd * bsum_j is one
-// fp32 MFMA pair per block (k = sub-block) that accumulates straight into
-// r: no int32 min accumulator, conversion or epilogue for it.
-template <int NB, int CH>
-__device__ __forceinline__ void q4w_mma_fm(const Q4W<CH> &w, const int8_t *aq, const float *ad, const float *amb,
-                                           float (&r)[4])
+// pair p's Q8_K block c): one fp32 MFMA pair per block (k = sub-block),
+// accumulated apart from the integer sums.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t q4, uint32_t m16)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q4) * __builtin_bit_cast(u16x2, m16));
+}
+
+template <int NB, int CH, int NT>
+__device__ __forceinline__ void q4w_mma_sp(const Q4W<CH> &w, const int8_t *aqA, const float *adA, const float *ambA,
+                                           float (&rA)[4], const int8_t *aqB, const float *adB, const float *ambB,
+                                           float (&rB)[4])
 {
     const int lane = lane_id(), lr = lane & 15, q = lane >> 4;
-    // the min terms accumulate in the matrix core (rm), the scaled
-    // sub-block sums in the VALU (r): neither waits on the other
-    v4f rm = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f rmA = {0.0f, 0.0f, 0.0f, 0.0f}, rmB = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const uint32_t y = w.hdr[c].y, z = w.hdr[c].z, x = w.hdr[c].w;
@@ -323,43 +340,71 @@ __device__ __forceinline__ void q4w_mma_fm(const Q4W<CH> &w, const int8_t *aq, c
         const uint32_t sc_hi = (x & 0x0F0F0F0Fu) | (((y >> 6) & 0x03030303u) << 4);
         const uint32_t m_hi = ((x >> 4) & 0x0F0F0F0Fu) | (((z >> 6) & 0x03030303u) << 4);
         const float d = h2f(w.hdr[c].x & 0xffff), ndmin = -h2f(w.hdr[c].x >> 16);
-        // min term: B[k = q][row] = -dmin * m_{4h + q}
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
             const float bm = ndmin * (float)(((hh ? m_hi : m_lo) >> (8 * q)) & 63);
-            rm = __builtin_amdgcn_mfma_f32_16x16x4f32(amb[(c * 2 + hh) * 64 + lane], bm, rm, 0, 0, 0);
+            rmA = __builtin_amdgcn_mfma_f32_16x16x4f32(ambA[(c * 2 + hh) * 64 + lane], bm, rmA, 0, 0, 0);
+            if constexpr (NT == 2)
+                rmB = __builtin_amdgcn_mfma_f32_16x16x4f32(ambB[(c * 2 + hh) * 64 + lane], bm, rmB, 0, 0, 0);
         }
-        int accs[4] = {0, 0, 0, 0};
+        const uint32_t sl[2] = {sc_lo & 0x07070707u, sc_hi & 0x07070707u};
+        const uint32_t sh[2] = {(sc_lo >> 3) & 0x07070707u, (sc_hi >> 3) & 0x07070707u};
+        v4i a1A = {0, 0, 0, 0}, a2A = a1A, a1B = a1A, a2B = a1A;
 #pragma unroll
-        for (int hb = 0; hb < 2; hb++) {
-            v4i p[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const int j = 4 * hb + jj;
-                const long a = *(const long *)(aq + lr * arow<NB>() + c * QK_K + 32 * j + 8 * q);
-                p[jj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, pack_nib(w.qs[c][j >> 1], j & 1), v4i{0, 0, 0, 0},
-                                                              0, 0, 0);
+        for (int t = 0; t < 4; t++) {
+            // sub-blocks 2t (low nibbles of group t) and 2t+1 (high); their
+            // scale bytes broadcast to both 16-bit halves by a byte permute
+            const long lo = pack_nib(w.qs[c][t], 0), hi = pack_nib(w.qs[c][t], 1);
+            const uint32_t b0 = (2 * t) & 3, b1 = (2 * t + 1) & 3;
+            const uint32_t s0 = b0 | 0x0C00u | (b0 << 16) | 0x0C000000u, s1 = b1 | 0x0C00u | (b1 << 16) | 0x0C000000u;
+            const uint32_t ml0 = __builtin_amdgcn_perm(0u, sl[t >> 1], s0), ml1 = __builtin_amdgcn_perm(0u, sl[t >> 1], s1);
+            const uint32_t mh0 = __builtin_amdgcn_perm(0u, sh[t >> 1], s0), mh1 = __builtin_amdgcn_perm(0u, sh[t >> 1], s1);
+            const uint32_t l0 = (uint32_t)lo, l1 = (uint32_t)((unsigned long)lo >> 32);
+            const uint32_t h0 = (uint32_t)hi, h1 = (uint32_t)((unsigned long)hi >> 32);
+            const v4i B1 = {(int)mul_bytes(l0, ml0), (int)mul_bytes(l1, ml0), (int)mul_bytes(h0, ml1),
+                            (int)mul_bytes(h1, ml1)};
+            const v4i B2 = {(int)mul_bytes(l0, mh0), (int)mul_bytes(l1, mh0), (int)mul_bytes(h0, mh1),
+                            (int)mul_bytes(h1, mh1)};
+            {
+                const long x0 = *(const long *)(aqA + lr * arow<NB>() + c * QK_K + 64 * t + 8 * q);
+                const long x1 = *(const long *)(aqA + lr * arow<NB>() + c * QK_K + 64 * t + 32 + 8 * q);
+                const v4i av = {(int)(uint32_t)x0, (int)(uint32_t)((unsigned long)x0 >> 32), (int)(uint32_t)x1,
+                                (int)(uint32_t)((unsigned long)x1 >> 32)};
+                a1A = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B1, a1A, 0, 0, 0);
+                a2A = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B2, a2A, 0, 0, 0);
             }
-            const uint32_t sw = hb ? sc_hi : sc_lo;
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const int sc = (int)((sw >> (8 * jj)) & 63);
-                accs[0] = __mul24(sc, p[jj][0]) + accs[0];
-                accs[1] = __mul24(sc, p[jj][1]) + accs[1];
-                accs[2] = __mul24(sc, p[jj][2]) + accs[2];
-                accs[3] = __mul24(sc, p[jj][3]) + accs[3];
+            if constexpr (NT == 2) {
+                const long x0 = *(const long *)(aqB + lr * arow<NB>() + c * QK_K + 64 * t + 8 * q);
+                const long x1 = *(const long *)(aqB + lr * arow<NB>() + c * QK_K + 64 * t + 32 + 8 * q);
+                const v4i av = {(int)(uint32_t)x0, (int)(uint32_t)((unsigned long)x0 >> 32), (int)(uint32_t)x1,
+                                (int)(uint32_t)((unsigned long)x1 >> 32)};
+                a1B = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B1, a1B, 0, 0, 0);
+                a2B = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B2, a2B, 0, 0, 0);
             }
+            // keep each sub-block pair's operands short-lived (the scheduler
+            // would otherwise build all four pairs' ahead and spill)
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const float4 xd = *(const float4 *)(ad + c * 16 + 4 * q);
-        r[0] += (d * xd.x) * (float)accs[0];
-        r[1] += (d * xd.y) * (float)accs[1];
-        r[2] += (d * xd.z) * (float)accs[2];
-        r[3] += (d * xd.w) * (float)accs[3];
+        {
+            const float4 xd = *(const float4 *)(adA + c * 16 + 4 * q);
+            rA[0] += (d * xd.x) * (float)(a1A[0] + 8 * a2A[0]);
+            rA[1] += (d * xd.y) * (float)(a1A[1] + 8 * a2A[1]);
+            rA[2] += (d * xd.z) * (float)(a1A[2] + 8 * a2A[2]);
+            rA[3] += (d * xd.w) * (float)(a1A[3] + 8 * a2A[3]);
+        }
+        if constexpr (NT == 2) {
+            const float4 xd = *(const float4 *)(adB + c * 16 + 4 * q);
+            rB[0] += (d * xd.x) * (float)(a1B[0] + 8 * a2B[0]);
+            rB[1] += (d * xd.y) * (float)(a1B[1] + 8 * a2B[1]);
+            rB[2] += (d * xd.z) * (float)(a1B[2] + 8 * a2B[2]);
+            rB[3] += (d * xd.w) * (float)(a1B[3] + 8 * a2B[3]);
+        }
     }
-    r[0] += rm[0];
-    r[1] += rm[1];
-    r[2] += rm[2];
-    r[3] += rm[3];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        rA[i] += rmA[i];
+        if constexpr (NT == 2) rB[i] += rmB[i];
+    }
 }
 
 // ------------------------------------------------------- Q6_K x Q8_K tile --
@@ -484,7 +529,7 @@ __device__ __forceinline__ void q6b_mma(const Q6B<NB> &u, const int8_t *aq, cons
 // them while the chunk's pairs stream past in M tiles of 16: the tile's
 // Q8_K(x) rows go global -> LDS by DMA (no registers), double buffered, the
 // next tile's DMA in flight during the current tile's MFMAs.  n_embd 4096
-// runs as two passes of 8 super-blocks.
+// runs as four passes of 4 super-blocks.
 constexpr int GR_ROWS = 32;
 
 // stage the Q8_K rows (super-blocks [kb0, kb0 + KH)) and scales of the M
@@ -546,7 +591,7 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
     const int8_t *__restrict__ xq, const float *__restrict__ xd, const float *__restrict__ xmb,
     float *__restrict__ h)
 {
-    constexpr int KH = NBE < 8 ? NBE : 8;      // super-blocks held per pass
+    constexpr int KH = NBE <= 8 ? NBE : 4;     // super-blocks held per pass (n_embd 4096: 4 passes of 4)
     constexpr int NPASS = NBE / KH;
     // the two buffers are separate LDS objects: the compiler then knows
     // that reading one need not wait for the DMA into the other
@@ -595,22 +640,25 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) {
         if (ps > 0) q4w_load(w, wrow, ps * KH);
+        // tiles in pairs, both buffers staged at once: a pair shares the
+        // scaled weight operands
         stage_dma<KH>(s_tok, NBE, ps * KH, xq, xd, xmb, s_aq0, s_ad0, s_mb0);
+        if (mtn > 1) stage_dma<KH>(s_tok + PB, NBE, ps * KH, xq, xd, xmb, s_aq1, s_ad1, s_mb1);
 #pragma unroll
-        for (int m = 0; m < MC / PB; m++) {
-            if (m < mtn) {                     // workgroup-uniform
-                // tile m has landed (the barrier waits for this wave's DMA,
-                // then for every wave) and tile m-1's buffer is free
-                __syncthreads();
-                if (m + 1 < mtn)
-                    stage_dma<KH>(s_tok + PB * (m + 1), NBE, ps * KH, xq, xd, xmb, (m & 1) ? s_aq0 : s_aq1,
-                                  (m & 1) ? s_ad0 : s_ad1, (m & 1) ? s_mb0 : s_mb1);
-                // the weight registers are opaque to the compiler from here,
-                // so it derives the MFMA operands anew per tile instead of
-                // keeping all of them (twice the registers) live across tiles
+        for (int mp = 0; mp < MC / PB / 2; mp++) {
+            if (2 * mp < mtn) {                // workgroup-uniform
+                __syncthreads();               // the pair's DMA has landed (every wave's)
                 q4w_opaque(w);
-                q4w_mma_fm<KH, KH>(w, (m & 1) ? s_aq1 : s_aq0, (m & 1) ? s_ad1 : s_ad0, (m & 1) ? s_mb1 : s_mb0,
-                                   r[m]);
+                if (2 * mp + 1 < mtn)
+                    q4w_mma_sp<KH, KH, 2>(w, s_aq0, s_ad0, s_mb0, r[2 * mp], s_aq1, s_ad1, s_mb1, r[2 * mp + 1]);
+                else
+                    q4w_mma_sp<KH, KH, 1>(w, s_aq0, s_ad0, s_mb0, r[2 * mp], s_aq1, s_ad1, s_mb1, r[2 * mp + 1]);
+                if (2 * mp + 2 < mtn) {
+                    __syncthreads();           // both buffers read: stage the next pair
+                    stage_dma<KH>(s_tok + PB * (2 * mp + 2), NBE, ps * KH, xq, xd, xmb, s_aq0, s_ad0, s_mb0);
+                    if (2 * mp + 3 < mtn)
+                        stage_dma<KH>(s_tok + PB * (2 * mp + 3), NBE, ps * KH, xq, xd, xmb, s_aq1, s_ad1, s_mb1);
+                }
             }
         }
         __syncthreads();                       // the buffers are free for the next pass / the hand-off
