@@ -319,3 +319,27 @@ def test_moe_layer_descriptor_reuse(qm):
     assert np.array_equal(run(desc, outs[3]), a0)
     for r in rls:
         r.close()
+
+
+def test_moe_prefill_concentrated_router(qm, orc):
+    """Every token routed to the same 8 experts (a +40 logit bias on experts
+    3, 17, ..): 8 buckets of 256 pairs plus the shared one, so the grouped
+    GEMMs run only full 64-pair chunks, four per expert -- the case where
+    one expert's rows are read by several chunks and the chunk list holds
+    no partial chunk."""
+    rl = qm.ResidentLayer(seed=123, layer=0, router_bias_std=1.0)
+    hot = [3, 17, 60, 61, 99, 128, 200, 255]
+    bias = np.random.default_rng(9).standard_normal(256).astype(np.float32) * 0.1
+    bias[hot] += np.float32(40.0) + np.arange(8, dtype=np.float32)
+    rl.router_bias.upload(bias)
+    hl = host_of(orc, rl)
+    T = 256
+    x = orc.fill_normal(808, T * 2048, 0.0, 1.0)
+    orc.set_threads(8)
+    try:
+        check_layer_staged(qm, orc, rl, hl, x, T, stage1_tokens=range(0, T, 16))
+    finally:
+        orc.set_threads(1)
+    st = qm.moe_last_stage(256, 8, 512, n_tok=T)
+    assert sorted(set(st["sel"].ravel().tolist())) == sorted(hot)
+    rl.close()
