@@ -667,12 +667,12 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             const bool last = l + 1 == n_layer;
             TR(0);
 
-            // ---- rows that do not depend on the selection, requested at
-            // layer start while the HBM is otherwise idle: the shared
-            // expert's gate/up row pair of this wave and, in the shared slot's
-            // down workgroups, their down rows
+            // ---- rows that do not depend on the selection: in the shared
+            // slot's down workgroups their down rows, requested at layer
+            // start; the shared expert's gate/up row pairs follow once x_l is
+            // published (below), so that they do not compete with the core's
+            // reads for the router and the logits
             uint4 sh_h = make_uint4(0, 0, 0, 0), sh_0 = sh_h, sh_1 = sh_h;
-            if (sh_row < F) gu_load(sh_h, sh_0, sh_1, (const uint8_t *)(half ? L.up_shexp : L.gate_shexp), sh_row);
             const int dslot = dunit >= 0 ? dunit / DWG_PER_SLOT : sh_down ? K : S;   // S: no down role
             const bool down = dslot < S && (dunit < 0 || dslot < K);
             DRaw<TD> dr[DN_ROUNDS];
@@ -703,6 +703,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             } else if (wv >= 2) {
                 uint32_t g1[1];
                 ok = poll<1>(tg->xq[rep], [&](int) { return lane == 0 ? XR_G + (b & 7) : -1; }, seq, g1, abort_flag);
+                if (sh_row < F) gu_load(sh_h, sh_0, sh_1, (const uint8_t *)(half ? L.up_shexp : L.gate_shexp), sh_row);
                 constexpr int XP = (XR_WORDS / 2 + 63) / 64;   // 6 word pairs per lane
                 uint32_t v[XP][2];
                 auto xp = [&](int k) {
