@@ -44,48 +44,55 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int PB = 16;            // pairs per MFMA tile (the 16-wide M side)
 
 // --------------------------------------------------------------- router --
-// One workgroup per 16 tokens x 16 experts; its four waves split k four
-// ways and lane group q of a wave owns a contiguous sixteenth of k, so each
-// lane streams its own slice of one x row and one router row (float4
-// loads, four independent accumulators).  The four waves' partial tiles
-// are summed through LDS in a fixed order.
-__global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restrict__ Wr,
-                                                          const float *__restrict__ bias,
-                                                          const float *__restrict__ x, int N, int E,
-                                                          int T, float *__restrict__ logits)
+// One workgroup per 16 tokens x 16 experts with W = N/256 waves; wave w
+// owns k = [256w, 256w + 256).  Lane group q takes float4 4u+q of that
+// range in request u, so the four lanes of one row read 64 contiguous bytes
+// per request (16 cache lines per request, not 64).  Each lane issues its 16
+// float4 of one x row and of one router row at once (no load waits on
+// another's round trip) and feeds them to four independent accumulators.
+// Rows past T or E are clamped to the last one: they only reach output
+// elements that are not stored.  The waves' partial tiles are summed
+// through LDS in a fixed order.
+template <int W>
+__global__ __launch_bounds__(64 * W) void router_mfma_kernel(const float *__restrict__ Wr,
+                                                             const float *__restrict__ bias,
+                                                             const float *__restrict__ x, int N, int E,
+                                                             int T, float *__restrict__ logits)
 {
-    __shared__ v4f s_red[3][64];
+    constexpr int V = 16;                      // float4 per lane and operand
+    __shared__ v4f s_red[W > 1 ? W - 1 : 1][64];
     const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
     const int eblocks = (E + 15) / 16;
     const int tb = (int)blockIdx.x / eblocks, eb = (int)blockIdx.x % eblocks;
-    if (tb * 16 >= T) return;
-    const int tok = tb * 16 + (lane & 15), e = eb * 16 + (lane & 15), q = lane >> 4;
-    const int seg = N / 16;                    // k per lane
-    const float4 *xr = (const float4 *)(x + (size_t)(tok < T ? tok : 0) * N + (4 * wv + q) * seg);
-    const float4 *wr = (const float4 *)(Wr + (size_t)(e < E ? e : 0) * N + (4 * wv + q) * seg);
-    const float xs = tok < T ? 1.0f : 0.0f, ws = e < E ? 1.0f : 0.0f;
+    const int tok = min(tb * 16 + (lane & 15), T - 1), e = min(eb * 16 + (lane & 15), E - 1), q = lane >> 4;
+    const float4 *xr = (const float4 *)(x + (size_t)tok * N) + 4 * V * wv + q;
+    const float4 *wr = (const float4 *)(Wr + (size_t)e * N) + 4 * V * wv + q;
+    float4 a[V], b[V];
+#pragma unroll
+    for (int u = 0; u < V; u++) {
+        a[u] = xr[4 * u];
+        b[u] = wr[4 * u];
+    }
+    __builtin_amdgcn_sched_barrier(0);         // every request issued before the first MFMA
     v4f acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
                   {0.0f, 0.0f, 0.0f, 0.0f}};
-    for (int s = 0; s < seg / 4; s += 4) {
-        float4 a[4], b[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            a[u] = xr[s + u];
-            b[u] = wr[s + u];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x * xs, b[u].x * ws, acc[u], 0, 0, 0);
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y * xs, b[u].y * ws, acc[u], 0, 0, 0);
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z * xs, b[u].z * ws, acc[u], 0, 0, 0);
-            acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w * xs, b[u].w * ws, acc[u], 0, 0, 0);
-        }
+    for (int u = 0; u < V; u++) {
+        v4f &c = acc[u & 3];
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, c, 0, 0, 0);
     }
     const v4f part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    if (wv > 0) s_red[wv - 1][lane] = part;
-    __syncthreads();
-    if (wv > 0) return;
-    const v4f sum = (part + s_red[0][lane]) + (s_red[1][lane] + s_red[2][lane]);
+    if (W > 1) {
+        if (wv > 0) s_red[wv - 1][lane] = part;
+        __syncthreads();
+        if (wv > 0) return;
+    }
+    v4f sum = part;
+#pragma unroll
+    for (int w = 0; w < W - 1; w++) sum += s_red[w][lane];
     // lane holds logits[tb*16 + 4q + i][eb*16 + lane%16]
     const int eo = eb * 16 + (lane & 15);
 #pragma unroll
@@ -825,8 +832,17 @@ int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *lo
 {
     const int N = L->n_embd, E = L->n_expert;
     const int tiles = ((T + 15) / 16) * ((E + 15) / 16);
-    hipLaunchKernelGGL(router_mfma_kernel, dim3(tiles), dim3(256), 0, s, L->gate_inp, L->router_bias,
-                       x, N, E, T, logits);
+    auto go = [&](auto kern, int W) {
+        hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * W), 0, s, L->gate_inp, L->router_bias, x, N, E, T, logits);
+    };
+    switch (N / QK_K) {                 // N = 256 * W, W a power of two up to 16 (moe_check_layer)
+    case 1: go(router_mfma_kernel<1>, 1); break;
+    case 2: go(router_mfma_kernel<2>, 2); break;
+    case 4: go(router_mfma_kernel<4>, 4); break;
+    case 8: go(router_mfma_kernel<8>, 8); break;
+    case 16: go(router_mfma_kernel<16>, 16); break;
+    default: return fail(QMAG_ERR_ARG, "router: n_embd=%d", N);
+    }
     QMAG_HIP(hipGetLastError());
     return QMAG_OK;
 }
