@@ -80,6 +80,7 @@ def check_layer(qm, orc, rl, hl, x, T):
     dict(n_embd=256, n_ff=512, n_expert=12, n_used=8, t_down=12),
     dict(n_embd=1024, n_ff=1024, n_expert=64, n_used=6, t_down=14),
     dict(n_embd=2048, n_ff=512, n_expert=32, n_used=8, t_down=12),
+    dict(n_embd=4096, n_ff=256, n_expert=16, n_used=4, t_down=14),
 ])
 def test_moe_layer_small_shapes(qm, orc, cfg):
     hl = make_host_layer(orc, seed=11, **cfg)
@@ -226,6 +227,7 @@ def check_layer_staged(qm, orc, rl, hl, x, T, stage1_tokens=None):
     dict(n_embd=256, n_ff=512, n_expert=12, n_used=8, t_down=12),
     dict(n_embd=1024, n_ff=1024, n_expert=64, n_used=6, t_down=14),
     dict(n_embd=2048, n_ff=512, n_expert=32, n_used=8, t_down=12),
+    dict(n_embd=4096, n_ff=256, n_expert=16, n_used=4, t_down=14),
 ])
 def test_moe_grouped_small_shapes(qm, orc, cfg):
     """Batches of >= 8 tokens run the grouped int8-MFMA expert GEMM; ragged
