@@ -313,6 +313,8 @@ __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, floa
     // softmax sum cancelled.  Each lane sorts its four candidates (experts
     // lane + 64j) once; a round is then one wave max over the lane heads,
     // one ballot for the winning lane, and a shift of that lane's list.
+    // Equal logits go to the lower expert index first (the reference's
+    // strict-> scan from e = 0), in the lane's sort and across lanes.
     const int lane = lane_id();
     float v[4];
     int id[4];
@@ -321,8 +323,8 @@ __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, floa
         v[j] = lane + 64 * j < E ? lg[j] : -INFINITY;
         id[j] = lane + 64 * j;
     }
-    auto cswap = [&](int i, int j) {           // descending; an equal pair keeps its order
-        const bool sw = v[j] > v[i];
+    auto cswap = [&](int i, int j) {           // descending; equal values by index
+        const bool sw = v[j] > v[i] || (v[j] == v[i] && id[j] < id[i]);
         const float vi = v[i], vj = v[j];
         const int ii = id[i], ij = id[j];
         v[i] = sw ? vj : vi;
@@ -338,9 +340,20 @@ __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, floa
     float my_l = -INFINITY, l0 = 0.0f;
     for (int k = 0; k < K; k++) {
         const float m = group_max<64>(v[0]);
-        const unsigned long long bal = __ballot(v[0] == m);
+        unsigned long long bal = __ballot(v[0] == m);
         // a NaN maximum equals nothing: fall back to lane 0's head, in range
-        const int win = bal ? __builtin_ctzll(bal) : 0;
+        int win = bal ? __builtin_ctzll(bal) : 0;
+        if (bal & (bal - 1)) {                  // exact tie: the lowest index wins
+            int best = __builtin_amdgcn_readlane(id[0], win);
+            for (bal &= bal - 1; bal; bal &= bal - 1) {
+                const int ln = __builtin_ctzll(bal);
+                const int c = __builtin_amdgcn_readlane(id[0], ln);
+                if (c < best) {
+                    best = c;
+                    win = ln;
+                }
+            }
+        }
         const int e = __builtin_amdgcn_readlane(id[0], win);
         const bool me = lane == win;
         v[0] = me ? v[1] : v[0];

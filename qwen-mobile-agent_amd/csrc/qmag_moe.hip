@@ -39,13 +39,33 @@ __global__ __launch_bounds__(256) void router_kernel(const float *__restrict__ W
 }
 
 // ----------------------------------------------------------------- top-k --
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m)
+// (p, e) ordering of the selection: larger p first, the lower expert index
+// among equal p (the reference's strict-> scan from e = 0)
+__device__ __forceinline__ bool tk_before(float pa, int ea, float pb, int eb)
 {
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
-    return ((unsigned long long)hi << 32) | lo;
+    return pa > pb || (pa == pb && ea < eb);
 }
 
+__device__ __forceinline__ void tk_cswap(float (&p)[4], int (&id)[4], int a, int b)
+{
+    if (tk_before(p[b], id[b], p[a], id[a])) {
+        const float tp = p[a];
+        const int ti = id[a];
+        p[a] = p[b];
+        id[a] = id[b];
+        p[b] = tp;
+        id[b] = ti;
+    }
+}
+
+// One workgroup per token.  Every load is issued first (each wave's x
+// blocks with the matching shared-gate weights, and the logits in wave 0),
+// so the workgroup waits for one round trip.  Each wave quantises its
+// blocks and adds its share of the shared gate from registers; wave 0 then
+// runs the softmax and the top-K: each lane sorts its four (p, e) once, and
+// a pick is one wave max over the lane heads, a ballot for the lanes holding
+// it (more than one only on an exact tie, then the lowest index among them)
+// and a shift of the winning lane's list.
 __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits,
                                                    const float *__restrict__ x,
                                                    const float *__restrict__ wsh, int N, int E,
@@ -55,42 +75,60 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
                                                    int8_t *__restrict__ xq, float *__restrict__ xd,
                                                    int16_t *__restrict__ xs, float *__restrict__ xmb)
 {
-    __shared__ int8_t s_xq[4096];
-    __shared__ float s_xd[16];
+    constexpr int MB = 4;                     // 256-blocks per wave (n_embd <= 4096)
     __shared__ float s_red[4];
     const int t = blockIdx.x;
     const int lane = lane_id(), wv = threadIdx.x >> 6;
     const int NB = N / QK_K;
 
-    // Q8_K of x[t]: one wave per 256-block
-    for (int b = wv; b < NB; b += 4) {
-        const float4 v = ((const float4 *)(x + (size_t)t * N + b * QK_K))[lane];
-        const Q8Lane r = q8k_quant_lane(v);
-        ((uint32_t *)(xq + (size_t)t * N + b * QK_K))[lane] = r.packed;
-        ((uint32_t *)(s_xq + b * QK_K))[lane] = r.packed;
-        if (lane == 0) {
-            xd[(size_t)t * NB + b] = r.d;
-            s_xd[b] = r.d;
-        }
-        if ((lane & 3) == 0) xs[(size_t)t * (N / 16) + b * 16 + (lane >> 2)] = (int16_t)r.gsum;
-        // the grouped prefill's Q4_K min-term operand: d * (sum of the 32
-        // values of each sub-block), lanes 8j .. 8j+7 holding sub-block j
-        const int s32 = r.gsum + __shfl_xor(r.gsum, 4);
-        if (xmb && (lane & 7) == 0) xmb[(size_t)t * (N / 32) + b * 8 + (lane >> 3)] = r.d * (float)s32;
+    float4 xv[MB], gw[MB];
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+        const int b = min(wv + 4 * i, NB - 1);   // unconditional; blocks past NB unused
+        xv[i] = ((const float4 *)(x + (size_t)t * N + b * QK_K))[lane];
+        gw[i] = ((const float4 *)(wsh + b * QK_K))[lane];
     }
+    float l[4];
+    if (wv == 0) {
+        const float *lg = logits + (size_t)t * E;
+#pragma unroll
+        for (int j = 0; j < 4; j++) l[j] = lg[min(lane + 64 * j, E - 1)];
+    }
+
+    // Q8_K of x[t] (one wave per 256-block) and the shared gate's
+    // sum_i wsh[i] * xq[i] * xd[i/256] over the wave's blocks
+    float g = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+        const int b = wv + 4 * i;
+        if (b < NB) {
+            const Q8Lane r = q8k_quant_lane(xv[i]);
+            ((uint32_t *)(xq + (size_t)t * N + b * QK_K))[lane] = r.packed;
+            if (lane == 0) xd[(size_t)t * NB + b] = r.d;
+            if ((lane & 3) == 0) xs[(size_t)t * (N / 16) + b * 16 + (lane >> 2)] = (int16_t)r.gsum;
+            // the grouped prefill's Q4_K min-term operand: d * (sum of the
+            // 32 values of each sub-block), lanes 8j .. 8j+7 holding sub-block j
+            const int s32 = r.gsum + __shfl_xor(r.gsum, 4);
+            if (xmb && (lane & 7) == 0) xmb[(size_t)t * (N / 32) + b * 8 + (lane >> 3)] = r.d * (float)s32;
+            const int8_t *q8 = (const int8_t *)&r.packed;
+            g += gw[i].x * (float)q8[0] * r.d + gw[i].y * (float)q8[1] * r.d + gw[i].z * (float)q8[2] * r.d +
+                 gw[i].w * (float)q8[3] * r.d;
+        }
+    }
+    g = group_sum<64>(g);
+    if (lane == 0) s_red[wv] = g;
 
     if (wv == 0) {
         // softmax over E <= 256 logits, 4 per lane
-        const float *lg = logits + (size_t)t * E;
-        float l[4], p[4];
         float mx = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int e = lane + 64 * j;
-            l[j] = e < E ? lg[e] : -INFINITY;
+            if (lane + 64 * j >= E) l[j] = -INFINITY;
             mx = fmaxf(mx, l[j]);
         }
         mx = group_max<64>(mx);
+        float p[4];
+        int id[4];
         float se = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -99,49 +137,58 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
             se += p[j];
         }
         se = group_sum<64>(se);
-        unsigned long long key[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int e = lane + 64 * j;
-            p[j] = p[j] / se;
-            // p >= 0: its bit pattern orders like the value; ~e makes the
-            // lowest index win among equal probabilities
-            key[j] = e < E ? (((unsigned long long)__float_as_uint(p[j]) << 32) | (uint32_t)~e) : 0ull;
+            id[j] = e;
+            p[j] = e < E ? p[j] / se : -1.0f;  // p >= 0 for every expert
         }
-        float wk[8];
-        int sk[8];
+        tk_cswap(p, id, 0, 1);
+        tk_cswap(p, id, 2, 3);
+        tk_cswap(p, id, 0, 2);
+        tk_cswap(p, id, 1, 3);
+        tk_cswap(p, id, 1, 2);
+        float wk = 0.0f;
+        int sk = 0;
         for (int k = 0; k < K; k++) {
-            unsigned long long b = key[0];
-#pragma unroll
-            for (int j = 1; j < 4; j++) b = key[j] > b ? key[j] : b;
-#pragma unroll
-            for (int m = 1; m < 64; m <<= 1) {
-                const unsigned long long o = shfl_xor_u64(b, m);
-                b = o > b ? o : b;
+            const float m = group_max<64>(p[0]);
+            unsigned long long bal = __ballot(p[0] == m);
+            // a NaN maximum equals nothing: fall back to lane 0's head, in range
+            int win = bal ? __builtin_ctzll(bal) : 0;
+            if (bal & (bal - 1)) {                // exact tie: the lowest index wins
+                int best = __builtin_amdgcn_readlane(id[0], win);
+                for (bal &= bal - 1; bal; bal &= bal - 1) {
+                    const int ln = __builtin_ctzll(bal);
+                    const int e = __builtin_amdgcn_readlane(id[0], ln);
+                    if (e < best) {
+                        best = e;
+                        win = ln;
+                    }
+                }
             }
-            const int e = (int)~(uint32_t)b;
-            sk[k] = e;
-            wk[k] = __uint_as_float((uint32_t)(b >> 32));
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (lane + 64 * j == e) key[j] = 0ull;
+            const int e = __builtin_amdgcn_readlane(id[0], win);
+            if (lane == k) {
+                sk = e;
+                wk = m;
+            }
+            if (lane == win) {
+                p[0] = p[1];
+                p[1] = p[2];
+                p[2] = p[3];
+                p[3] = -2.0f;
+                id[0] = id[1];
+                id[1] = id[2];
+                id[2] = id[3];
+            }
         }
-        if (lane == 0) {
-            float ws = 0.0f;
-            for (int k = 0; k < K; k++) ws += wk[k];
-            for (int k = 0; k < K; k++) {
-                sel[(size_t)t * K + k] = sk[k];
-                wout[(size_t)t * K + k] = wk[k] / ws;
-            }
+        // w_k = p_k / sum_sel p, the sum in pick order
+        float ws = 0.0f;
+        for (int k = 0; k < K; k++) ws += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wk), k));
+        if (lane < K) {
+            sel[(size_t)t * K + lane] = sk;
+            wout[(size_t)t * K + lane] = wk / ws;
         }
     }
-    __syncthreads();
-
-    // shared-expert gate: sum_i wsh[i] * xq[i] * xd[i/256], then sigmoid
-    float g = 0.0f;
-    for (int i = threadIdx.x; i < N; i += 256) g += wsh[i] * (float)s_xq[i] * s_xd[i / QK_K];
-    g = group_sum<64>(g);
-    if (lane == 0) s_red[wv] = g;
     __syncthreads();
     if (threadIdx.x == 0) {
         const float s = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);

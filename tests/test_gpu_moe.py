@@ -345,3 +345,41 @@ def test_moe_prefill_concentrated_router(qm, orc):
     st = qm.moe_last_stage(256, 8, 512, n_tok=T)
     assert sorted(set(st["sel"].ravel().tolist())) == sorted(hot)
     rl.close()
+
+
+LEAD = [12, 140, 77, 205]                          # biases 53, 52, 51, 50
+TIED = [250, 7, 71, 135, 199, 3, 67, 131, 195, 100]  # all 40.0
+
+
+@pytest.mark.parametrize("path,T", [("fused", 1), ("sequence", 1), ("sequence", 3), ("grouped", 16)])
+def test_moe_route_exact_ties_lowest_index(qm, orc, path, T):
+    """Logits tied exactly (a zero router, so the logits are the biases):
+    among equal probabilities the reference's strict-> scan keeps the lowest
+    expert index (nn.c:526-533).  Four experts lead; ten more share one
+    bias, spread over the lanes and list positions of the top-K (expert e
+    sits in lane e % 64, position e // 64; lanes 3 and 7 each hold four of
+    them), so the last four slots go to 3, 7, 67, 71 in that order."""
+    rl = qm.ResidentLayer(seed=321, layer=0, router_bias_std=1.0)
+    rl.gate_inp.upload(np.zeros(256 * 2048, np.float32))
+    bias = (np.random.default_rng(5).standard_normal(256) * 0.1).astype(np.float32)
+    bias[LEAD] = np.array([53.0, 52.0, 51.0, 50.0], np.float32)
+    bias[TIED] = np.float32(40.0)
+    rl.router_bias.upload(bias)
+    hl = host_of(orc, rl)
+    x = orc.fill_normal(909 + T, T * 2048, 0.0, 1.0)
+    qm.set_fused(path == "fused")
+    try:
+        got = run_layer(qm, rl, x, T)
+        st = qm.moe_last_stage(256, 8, 512, n_tok=T)
+    finally:
+        qm.set_fused(True)
+    want = LEAD + [3, 7, 67, 71]
+    for t in range(T):
+        sel_o, w_o, _ = orc.moe_route(hl, x[t * 2048:(t + 1) * 2048])
+        assert list(sel_o) == want                 # the oracle keeps the same rule
+        assert st["sel"][t].tolist() == want, f"token {t}"
+        assert np.allclose(st["w"][t], w_o, rtol=1e-5, atol=1e-7), f"token {t}"
+    ref = orc.moe_ffn(hl, x, T)
+    for t in range(T):
+        assert max_rel_err(got[t], ref[t]) < TOL, f"token {t}"
+    rl.close()
