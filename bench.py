@@ -40,7 +40,7 @@ METRIC = "MoE FFN decode tokens/s + achieved HBM GB/s (% of peak), Q4_K/Q6_K, 1 
 # from two rocprofv3 counter passes over bench.py (FETCH_SIZE x 2.000 +
 # WRITE_SIZE x 1.000, the factors read off a 1 GiB copy kernel in the same
 # runs); re-measured whenever the kernel changes.
-FUSED_TRAFFIC_BYTES = 869.9e6
+FUSED_TRAFFIC_BYTES = 869.6e6
 
 
 def log(msg: str) -> None:
@@ -210,6 +210,9 @@ def aux_prefill(T: int = 512, n_layers: int = 3, iters: int = 5) -> dict:
            "int8_ops": ops, "mfma_tops": ops / (us * 1e-6) / 1e12, "mfma_frac_of_peak": ops / (us * 1e-6) / INT8_PEAK,
            "weight_bytes": nbytes, "hbm_gbps": nbytes / (us * 1e-6) / 1e9,
            "hbm_frac_of_peak": nbytes / (us * 1e-6) / HBM_PEAK, "per_kernel_us": per_k,
+           "per_kernel_note": "HIP event pair around each launch on the library stream, one extra pass; "
+                              "each pair adds a few us of its own, so short kernels read high (a kernel "
+                              "trace gives their own durations; the sum exceeds us_per_layer)",
            "gemm_kernels_mfma_frac": ops / (gemm_us * 1e-6) / INT8_PEAK if gemm_us else None}
     log(f"C5 prefill: {us:.1f} us/layer ({res['tokens_per_s']:.0f} tok/s), {d:.0f} distinct experts, "
         f"int8 {res['mfma_tops']:.1f} TOP/s ({100 * res['mfma_frac_of_peak']:.1f}% of peak), "
