@@ -814,17 +814,44 @@ __global__ __launch_bounds__(256, 2) void down_rows_kernel(
 }
 
 // -------------------------------------------------------------- combine --
+// One thread per 4 consecutive outputs of one token: the 9 slot rows (and the
+// residual) are requested as float4 before any is used; each element is
+// summed in the reference's order with unfused multiply and add.
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y, const float *__restrict__ w,
                                                       const float *__restrict__ gs, int T, int K, int N,
                                                       const float *__restrict__ resid, float *__restrict__ out)
 {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t i = 4 * ((size_t)blockIdx.x * 256 + threadIdx.x);   // N % 4 == 0
     if (i >= (size_t)T * N) return;
     const int t = (int)(i / N), r = (int)(i % N), S = K + 1;
-    float acc = 0.0f;
-    for (int k = 0; k < K; k++) acc = __fadd_rn(acc, __fmul_rn(w[t * K + k], y[((size_t)t * S + k) * N + r]));
-    acc = __fadd_rn(acc, __fmul_rn(gs[t], y[((size_t)t * S + K) * N + r]));
-    out[i] = resid ? __fadd_rn(acc, resid[i]) : acc;
+    float4 v[9];                                                       // K <= 8
+#pragma unroll
+    for (int k = 0; k < 9; k++) v[k] = *(const float4 *)(y + ((size_t)t * S + min(k, K)) * N + r);
+    const float4 rs = resid ? *(const float4 *)(resid + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        if (k < K) {
+            const float wk = w[t * K + k];
+            acc.x = __fadd_rn(acc.x, __fmul_rn(wk, v[k].x));
+            acc.y = __fadd_rn(acc.y, __fmul_rn(wk, v[k].y));
+            acc.z = __fadd_rn(acc.z, __fmul_rn(wk, v[k].z));
+            acc.w = __fadd_rn(acc.w, __fmul_rn(wk, v[k].w));
+        }
+    }
+    const float g = gs[t];
+    const float4 sh = v[8];                    // row min(8, K) = K: the shared slot
+    acc.x = __fadd_rn(acc.x, __fmul_rn(g, sh.x));
+    acc.y = __fadd_rn(acc.y, __fmul_rn(g, sh.y));
+    acc.z = __fadd_rn(acc.z, __fmul_rn(g, sh.z));
+    acc.w = __fadd_rn(acc.w, __fmul_rn(g, sh.w));
+    if (resid) {
+        acc.x = __fadd_rn(acc.x, rs.x);
+        acc.y = __fadd_rn(acc.y, rs.y);
+        acc.z = __fadd_rn(acc.z, rs.z);
+        acc.w = __fadd_rn(acc.w, rs.w);
+    }
+    *(float4 *)(out + i) = acc;
 }
 
 // ------------------------------------------------------------------ host --
@@ -907,7 +934,7 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
     }
     prof_end(PROF_DOWN, s);
     prof_begin(PROF_COMBINE, s);
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)(((size_t)T * N + 255) / 256)), dim3(256), 0, s, y, w, gs,
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)(((size_t)T * N / 4 + 255) / 256)), dim3(256), 0, s, y, w, gs,
                        T, K, N, resid, out);
     prof_end(PROF_COMBINE, s);
     QMAG_HIP(hipGetLastError());
