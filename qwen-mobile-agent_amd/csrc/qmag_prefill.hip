@@ -122,7 +122,7 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
 {
     __shared__ int s_cnt[257], s_off[258], s_fill[257], s_inc[257], s_finc[257];
     __shared__ int s_bin[MC], s_binf[MC];     // partial chunks by MC - size
-    __shared__ int s_nch;
+    __shared__ int s_nch, s_wtot[2][5];
     const int tid = (int)threadIdx.x, S = K + 1;
     for (int e = tid; e <= E; e += 1024) {
         s_cnt[e] = 0;
@@ -138,25 +138,36 @@ __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel
     for (int p = tid; p < T * K; p += 1024) atomicAdd(&s_cnt[expert(p)], 1);
     if (tid == 0) s_cnt[E] = T;      // shared expert: every token
     __syncthreads();
-    // inclusive prefix sums of the pair counts and the full-chunk counts over the E + 1 buckets (Hillis-Steele in LDS, 9
-    // steps); the partial chunks are counted per size
-    if (tid <= E) {
-        const int c = s_cnt[tid];
-        s_inc[tid] = c;
-        s_finc[tid] = c / MC;
+    // inclusive prefix sums of the pair counts and the full-chunk counts over
+    // the E + 1 <= 257 buckets: a scan inside each of waves 0-4, then the
+    // totals of the waves before; the partial chunks are counted per size
+    {
+        const int lane = tid & 63, wv = tid >> 6;
+        const int c = tid <= E ? s_cnt[tid] : 0;
         if (c % MC) atomicAdd(&s_bin[MC - c % MC], 1);
-    }
-    __syncthreads();
-    for (int d = 1; d <= 256; d <<= 1) {
-        int a = 0, m = 0;
-        if (tid <= E && tid >= d) {
-            a = s_inc[tid - d];
-            m = s_finc[tid - d];
+        int ci = c, fi = c / MC;
+        if (wv < 5) {                          // wave-uniform
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int o = __shfl_up(ci, d), of = __shfl_up(fi, d);
+                if (lane >= d) {
+                    ci += o;
+                    fi += of;
+                }
+            }
+            if (lane == 63) {
+                s_wtot[0][wv] = ci;
+                s_wtot[1][wv] = fi;
+            }
         }
         __syncthreads();
-        if (tid <= E && tid >= d) {
-            s_inc[tid] += a;
-            s_finc[tid] += m;
+        if (tid <= E) {
+            for (int w = 0; w < wv; w++) {
+                ci += s_wtot[0][w];
+                fi += s_wtot[1][w];
+            }
+            s_inc[tid] = ci;
+            s_finc[tid] = fi;
         }
         __syncthreads();
     }
