@@ -240,7 +240,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(this build runs on a single MI355X; see the sharding note in DESIGN.md)",
+              "(this build runs on a single MI355X; across GPUs the experts would shard by id, "
+              "with one 8 KB reduction of the layer output per layer)",
               file=sys.stderr)
         return 2
 
