@@ -383,3 +383,40 @@ def test_moe_route_exact_ties_lowest_index(qm, orc, path, T):
     for t in range(T):
         assert max_rel_err(got[t], ref[t]) < TOL, f"token {t}"
     rl.close()
+
+
+def test_fused_launch_options_bit_identical(qm):
+    """The persistent decode kernel gives the same bits launched
+    cooperatively (QMAG_OPT_COOP) and with phase tracing on (QMAG_OPT_TRACE,
+    which only adds timestamp stores) as in its default ordinary launch; the
+    trace holds the launch's phase stamps (100 MHz counter, one launch well
+    under a second)."""
+    rls = [qm.ResidentLayer(seed=77, layer=l) for l in range(4)]
+    cl = [r.c for r in rls]
+    x = np.random.default_rng(3).standard_normal(2048).astype(np.float32)
+
+    def run():
+        xb = qm.DBuf.from_array(x)
+        qm.moe_stack_dev(cl, xb.ptr, 1)
+        return xb.download(np.float32)
+
+    base = run()
+    qm.set_coop(True)
+    try:
+        coop = run()
+    finally:
+        qm.set_coop(False)
+    qm.set_trace(True)
+    try:
+        traced = run()
+        tr = qm.trace_read(4)
+    finally:
+        qm.set_trace(False)
+    again = run()
+    for other in (coop, traced, again):
+        assert np.array_equal(base.view(np.uint32), other.view(np.uint32))
+    stamps = tr[tr > 0]
+    assert stamps.size > 512
+    assert int(stamps.max() - stamps.min()) < 100_000_000
+    for r in rls:
+        r.close()
