@@ -40,6 +40,9 @@ extern "C" {
 #define QMAG_ERR_ARG (-2)      /* unsupported shape / type / null pointer    */
 #define QMAG_ERR_NODEV (-3)    /* no gfx950 device, or qmag_init not called  */
 #define QMAG_ERR_KERNEL (-4)   /* a kernel reported an internal guard trip   */
+/* Buffers passed to the device entries must stay valid until the next
+   qmag_sync or qmag_d2h: the library may re-run the calls issued since the
+   previous one (see qmag_fused_recoveries). */
 
 /* ------------------------------------------------------------------------ */
 /* Reference-compatible entries                                              */
@@ -59,6 +62,23 @@ float qma_q8k_dot(const void *row, int wtype, const int8_t *xq, const float *xd,
 void qma_q8k_gateup(const void *g, const void *u, const int8_t *xq, const float *xd,
                     const int16_t *xsum, int n, float *gate, float *up);
 
+/* The fp32 entries of src/quants.c (qma.h:348-351), same names, argument
+   order and host-pointer semantics; the block pointers are raw GGUF bytes
+   (the reference types them block_q4_K * / block_q6_K *, which link to the
+   same symbols).  Only whole super-blocks are processed (k / 256, n / 256),
+   as the reference loops.  They are skipped here when the engine's own
+   qma.h, which declares them with its block types, was included first. */
+#ifndef QMA_H
+/* replaces dequantize_row_q4_K, src/quants.c:29-47 (qma.h:348) */
+void dequantize_row_q4_K(const void *x, float *y, int64_t k);
+/* replaces dequantize_row_q6_K, src/quants.c:50-75 (qma.h:349) */
+void dequantize_row_q6_K(const void *x, float *y, int64_t k);
+/* replaces dot_q4_K_f32, src/quants.c:80-105 (qma.h:350) */
+float dot_q4_K_f32(const void *W, const float *x, int n);
+/* replaces dot_q6_K_f32, src/quants.c:108-133 (qma.h:351) */
+float dot_q6_K_f32(const void *W, const float *x, int n);
+#endif
+
 /* ------------------------------------------------------------------------ */
 /* Runtime                                                                   */
 /* ------------------------------------------------------------------------ */
@@ -75,9 +95,9 @@ int qmag_h2d(void *dst, const void *src, size_t bytes);      /* synchronous */
 int qmag_d2h(void *dst, const void *src, size_t bytes);      /* synchronous */
 int qmag_d2d(void *dst, const void *src, size_t bytes);      /* stream-ordered */
 int qmag_memset(void *dst, int value, size_t bytes);         /* stream-ordered */
-/* Wait for the library stream; also reports (QMAG_ERR_KERNEL) a grid-wide
-   wait of the fused decode kernel that hit its spin limit since the last
-   call, and re-arms its counters. */
+/* Wait for the library stream.  If a bounded wait of the persistent decode
+   kernel expired since the last check, the affected calls are re-run first
+   (see qmag_fused_recoveries); QMAG_ERR_KERNEL only if that fails too. */
 int qmag_sync(void);
 
 /* Timing on the library stream: record event `slot` (0..63) and read the
@@ -121,7 +141,21 @@ int qmag_prof_read(int kernel_id, long *count, double *total_ms);
    16 pairs, each expert's weights read once per chunk; 0 selects the
    per-token launch sequence (same results within the fp32 tolerance). */
 #define QMAG_OPT_GROUPED 4
+/* QMAG_OPT_TEST_ABORT (write-only; tests of the recovery path): value n > 0
+   makes the n-th persistent decode launch from now find its abort word
+   already set, as if its wait had expired, so it and the launches after it
+   exit without output and the next qmag_sync / qmag_d2h re-runs them through
+   the launch sequence; 0 cancels. */
+#define QMAG_OPT_TEST_ABORT 5
 int qmag_set_option(int option, int value);
+/* Persistent decode launches whose bounded cross-workgroup wait expired (50 ms
+   each; a workgroup that is not resident, e.g. CUs held by another process,
+   is the one way to get there) are reported at the next qmag_sync or
+   qmag_d2h, which then re-run the affected calls -- every call issued since
+   the previous status check, from the failing launch on -- through the
+   per-stage launch sequence, restoring in-place inputs from copies taken
+   before the calls ran, and return QMAG_OK.  This counts such recoveries. */
+int qmag_fused_recoveries(long *count);
 int qmag_trace_read(void *dst, size_t bytes);
 
 /* ------------------------------------------------------------------------ */
@@ -132,14 +166,28 @@ int qmag_trace_read(void *dst, size_t bytes);
 int qmag_q8k_quant_dev(const float *x, int n, int T, int8_t *xq, float *xd, int16_t *xsum);
 
 /* out[t][r] = row_r(W) . Q8_K(x[t]) for pre-quantised activations;
-   mm_worker, nn.c:276-289.  n_in in {256,512,1024,2048,4096,8192}. */
+   mm_worker, nn.c:276-289.  n_in: any multiple of 256 (powers of two up to
+   8192 run the tiled kernel, other lengths a kernel of one wave per row). */
 int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum,
                         const void *W, int n_in, int n_out, int T, int wtype, float *out);
 
 /* matmul seam, nn.c:307-345: quantise each x[t] once, then the matvec (for
-   T = 1 a single launch: the matvec quantises x itself, bit-identically). */
+   T = 1 and n_in a power of two up to 8192 a single launch: the matvec
+   quantises x itself, bit-identically).  n_in: any multiple of 256. */
 int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
                     float *out);
+
+/* Dequantisation of n weights (n % 256 == 0) to f32, bit-identical to
+   dequantize_row_q4_K / dequantize_row_q6_K (src/quants.c:29-75); the weight
+   definition embed_row uses (nn.c:2044-2054). */
+int qmag_dequant_dev(const void *W, int wtype, int64_t n, float *y);
+
+/* The fp32 dequantise-then-dot matmul (dot_q4_K_f32 / dot_q6_K_f32 per row,
+   src/quants.c:80-133; the QMA_NOQ8K path, nn.c:393-407, 475-492):
+   out[t][r] = sum_i deq(W_r)_i * x[t][i], no activation quantisation.
+   n_in: a multiple of 256 up to 8192. */
+int qmag_matmul_f32_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
+                        float *out);
 
 /* One MoE FFN layer's tensors, resident in HBM (device pointers).  Field
    meaning follows qma_t.layers[il] (src/qma.h:202-218); expert slabs are

@@ -49,7 +49,10 @@
 //
 // Every poll is bounded: an exhausted waiter raises an abort flag that all
 // pollers check, so the grid always drains; qmag_sync() reports it.
+#include <limits.h>
 #include <string.h>
+
+#include <vector>
 
 #include "qmag_internal.h"
 
@@ -78,7 +81,11 @@ constexpr int DN_ROUNDS = DROWS / 4 / 8;          // 16 rows per wave, 8 lanes p
 constexpr int RDN_WG0 = WGS / 2, SDN_WG0 = CORE;
 static_assert(RDN_WG0 + 8 * DWG_PER_SLOT <= WGS && SDN_WG0 + DWG_PER_SLOT <= RDN_WG0,
               "down workgroups out of range");
+// Every wait is bounded twice: by wall time (SPIN_TICKS of the 100 MHz
+// real-time counter, 50 ms, far beyond any legitimate hand-off of a few
+// microseconds) and, as a backstop, by a poll count.
 constexpr long SPIN_LIMIT = 1L << 22;
+constexpr uint64_t SPIN_TICKS = 5000000;
 
 // Q8_K records are laid out exactly as the LDS copy their readers keep, so a
 // reader copies word i to LDS word i:
@@ -121,13 +128,40 @@ __device__ __forceinline__ int ld_flag(const int *p)
     return __hip_atomic_load(const_cast<int *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The abort word: 0 while every wait has been met; otherwise epoch + 1 of the
+// first launch one of whose waits expired (the host replays from that launch
+// on).  Every poller checks it, so the grid drains once it is set, and a later
+// launch that finds it set exits before writing any output.
+struct Abort {
+    int *flag;
+    int code;       // this launch's epoch + 1
+};
+__device__ __forceinline__ void raise_abort(const Abort &ab)
+{
+    int expect = 0;
+    __hip_atomic_compare_exchange_strong(ab.flag, &expect, ab.code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+}
+// true when the wait that started at t0 must give up: another waiter raised
+// the abort word, or this one ran out of time (then it raises the word)
+__device__ __forceinline__ bool give_up(const Abort &ab, uint64_t t0)
+{
+    if (ld_flag(ab.flag) != 0) return true;
+    if (__builtin_amdgcn_s_memrealtime() - t0 > SPIN_TICKS) {
+        raise_abort(ab);
+        return true;
+    }
+    return false;
+}
+
 // One wave reads CNT tagged words per lane, p[idx(k)] (idx < 0: no word),
 // until every word carries `seq`; the low halves land in val[].  All loads of
 // a round are issued together, and a retry reloads only the stale words.
 template <int CNT, typename Idx>
 __device__ bool poll(const unsigned long long *p, Idx idx, uint32_t seq, uint32_t (&val)[CNT],
-                     int *abort_flag)
+                     const Abort &ab)
 {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     uint32_t pending = 0;
 #pragma unroll
     for (int k = 0; k < CNT; k++)
@@ -144,10 +178,10 @@ __device__ bool poll(const unsigned long long *p, Idx idx, uint32_t seq, uint32_
             }
         }
         if (__all(pending == 0)) return true;
-        if ((it & 31) == 31 && ld_flag(abort_flag) != 0) return false;
+        if ((it & 31) == 31 && give_up(ab, t0)) return false;
         __builtin_amdgcn_s_sleep(2);
     }
-    __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    raise_abort(ab);
     return false;
 }
 
@@ -177,8 +211,9 @@ __device__ __forceinline__ void st64(Rsrc rs, int word, uint32_t v, uint32_t seq
 // of the needed words land in val[k][0..1].
 template <int CNT, typename Code>
 __device__ bool pollq(Rsrc rs, int base_word, Code code, uint32_t seq, uint32_t (&val)[CNT][2],
-                      int *abort_flag)
+                      const Abort &ab)
 {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     uint32_t pending = 0;
 #pragma unroll
     for (int k = 0; k < CNT; k++)
@@ -213,10 +248,10 @@ __device__ bool pollq(Rsrc rs, int base_word, Code code, uint32_t seq, uint32_t 
             }
         }
         if (__all(pending == 0)) return true;
-        if ((it & 31) == 31 && ld_flag(abort_flag) != 0) return false;
+        if ((it & 31) == 31 && give_up(ab, t0)) return false;
         __builtin_amdgcn_s_sleep(2);
     }
-    __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    raise_abort(ab);
     return false;
 }
 
@@ -298,35 +333,40 @@ __device__ __forceinline__ float d_dot(const DRaw<TD> &d, const uint32_t *hq, co
     }
 }
 
-// softmax over E <= 256 logits (4 per lane of one wave, expert lane + 64j),
-// then the K largest probabilities in the order nn.c:525-536 picks them:
-// each pick is the maximum of what is left, the lowest index among equal
-// values.  The maximum is one DPP/permlane reduction; the lowest index
-// holding it comes from four ballots and scalar bit scans.  Lane k < K
-// receives pick k: its expert id and its weight renormalised over the K
-// picks (the sum taken in pick order).
+// Order-preserving int32 key of a finite float: a > b as floats exactly when
+// key(a) > key(b) as signed ints (-0 is folded to +0 first, so the two zeros,
+// equal as floats, get one key).  An integer wave max folds its DPP move into
+// the max itself; a float max would first quiet signalling NaNs in both
+// operands (three instructions per step instead of one).
+__device__ __forceinline__ int f2key(float v)
+{
+    const int b = __float_as_int(v + 0.0f);
+    return b >= 0 ? b : b ^ 0x7fffffff;
+}
+__device__ __forceinline__ float key2f(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7fffffff); }
+
+// Softmax top-K over E <= 256 logits (4 per lane of one wave: experts
+// lane + 64j), in the order nn.c:525-536 picks them: each pick is the largest
+// value left, the lowest index among equal values (the reference's strict-`>`
+// scan from e = 0).  The selection is made on the logits (softmax is
+// monotonic) through their integer keys; each lane sorts its four candidates
+// once, and a pick is one wave max over the lane heads, one ballot for the
+// winning lane and a shift of that lane's list.  Lane k < K receives pick k:
+// its expert id and its weight exp(l_k - l_max) / sum over the K picks, the
+// reference's p_k / sum_sel p with the full softmax sum cancelled (summed in
+// pick order).
 __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, float &my_w)
 {
-    // top-K on the logits themselves (softmax is monotonic, so the selection
-    // is the reference's), then w_k = exp(l_k - l_max) / sum over the K
-    // selected, which is p_k / sum_sel p of nn.c:522-536 with the full
-    // softmax sum cancelled.  Each lane sorts its four candidates (experts
-    // lane + 64j) once; a round is then one wave max over the lane heads,
-    // one ballot for the winning lane, and a shift of that lane's list.
-    // Equal logits go to the lower expert index first (the reference's
-    // strict-> scan from e = 0), in the lane's sort and across lanes.
     const int lane = lane_id();
-    float v[4];
-    int id[4];
+    int v[4], id[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        v[j] = lane + 64 * j < E ? lg[j] : -INFINITY;
+        v[j] = lane + 64 * j < E ? f2key(lg[j]) : INT_MIN;
         id[j] = lane + 64 * j;
     }
-    auto cswap = [&](int i, int j) {           // descending; equal values by index
+    auto cswap = [&](int i, int j) {           // descending; equal keys by index
         const bool sw = v[j] > v[i] || (v[j] == v[i] && id[j] < id[i]);
-        const float vi = v[i], vj = v[j];
-        const int ii = id[i], ij = id[j];
+        const int vi = v[i], vj = v[j], ii = id[i], ij = id[j];
         v[i] = sw ? vj : vi;
         v[j] = sw ? vi : vj;
         id[i] = sw ? ij : ii;
@@ -337,12 +377,11 @@ __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, floa
     cswap(0, 2);
     cswap(1, 3);
     cswap(1, 2);
-    float my_l = -INFINITY, l0 = 0.0f;
+    int my_key = INT_MIN, sel = 0;
     for (int k = 0; k < K; k++) {
-        const float m = group_max<64>(v[0]);
+        const int m = group_max_i<64>(v[0]);
         unsigned long long bal = __ballot(v[0] == m);
-        // a NaN maximum equals nothing: fall back to lane 0's head, in range
-        int win = bal ? __builtin_ctzll(bal) : 0;
+        int win = __builtin_ctzll(bal);         // some lane holds the maximum
         if (bal & (bal - 1)) {                  // exact tie: the lowest index wins
             int best = __builtin_amdgcn_readlane(id[0], win);
             for (bal &= bal - 1; bal; bal &= bal - 1) {
@@ -359,19 +398,19 @@ __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, floa
         v[0] = me ? v[1] : v[0];
         v[1] = me ? v[2] : v[1];
         v[2] = me ? v[3] : v[2];
-        v[3] = me ? -INFINITY : v[3];
+        v[3] = me ? INT_MIN : v[3];
         id[0] = me ? id[1] : id[0];
         id[1] = me ? id[2] : id[1];
         id[2] = me ? id[3] : id[2];
-        if (lane == k) {
-            my_sel = e;
-            my_l = m;
-        }
-        if (k == 0) l0 = m;
+        sel = lane == k ? e : sel;
+        my_key = lane == k ? m : my_key;
     }
-    const float ex = lane < K ? expf(my_l - l0) : 0.0f;
+    const float l0 = key2f(__builtin_amdgcn_readfirstlane(my_key));
+    if (lane < K) my_sel = sel;
+    const float ex = lane < K ? expf(key2f(my_key) - l0) : 0.0f;
     my_w = ex / group_sum<8>(ex);
 }
+
 
 template <int TD>
 __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer *__restrict__ layers,
@@ -398,6 +437,10 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
     const int rep = b % REP;
     const bool core = b < CORE;
     const Rsrc rs = __builtin_amdgcn_make_buffer_rsrc(tg, 0, (int)sizeof(Tagged), 0x00020000);
+    const Abort ab{abort_flag, (int)epoch + 1};
+    // set by an earlier launch whose wait expired: this launch exits at its
+    // first barrier, before any output is written (read now, used there)
+    const bool pre_abort = ld_flag(abort_flag) != 0;
     // the 256 logits of replica rep, lane's pairs l and l + 64 (experts
     // l + 64j, j = 0..3); a half is needed only for an expert below E
     auto logit_pairs = [&](int E) {
@@ -409,7 +452,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
     };
     auto read_logits = [&](int E, uint32_t seq, float (&lg)[4]) {
         uint32_t v[2][2];
-        const bool ok = pollq<2>(rs, TW_LOGITS + rep * 256, logit_pairs(E), seq, v, abort_flag);
+        const bool ok = pollq<2>(rs, TW_LOGITS + rep * 256, logit_pairs(E), seq, v, ab);
 #pragma unroll
         for (int j = 0; j < 4; j++)
             lg[j] = lane + 64 * j < E ? __uint_as_float(v[j >> 1][j & 1]) : -INFINITY;
@@ -548,16 +591,16 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 {
                     uint32_t g1[1];
                     ok = poll<1>(tg->x, [&](int) { return lane == 0 ? ((b + CORE / 2) % CORE) * CROWS + CROWS - 1 : -1; },
-                                 seq, g1, abort_flag);
+                                 seq, g1, ab);
                 }
-                ok = ok && pollq<6>(rs, TW_X, xp, seq, v, abort_flag);
+                ok = ok && pollq<6>(rs, TW_X, xp, seq, v, ab);
 #pragma unroll
                 for (int k = 0; k < 6; k++)
                     if (xp(k) >= 0)
                         ((float2 *)s_x)[xp(k) >> 2] = make_float2(__uint_as_float(v[k][0]), __uint_as_float(v[k][1]));
             }
             drain();                 // router rows have landed in LDS
-            if (!wg_all(ok, s_vote, 0)) return;
+            if (!wg_all(ok && !(l == 0 && pre_abort), s_vote, 0)) return;
             TR(1);
 
             // ---- logits (waves 0, 1, each published in every replica), then
@@ -565,12 +608,13 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             // each); Q8_K(x) block b and its shared-gate partial published
             // (wave 2, b < 8); softmax/top-K (wave 3)
             if (wv < NLOG) {
-                const int e = NLOG * b + wv;
+                const int lw = wv;
+                const int e = NLOG * b + lw;
                 if (e < E) {
                     float s = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
-                        const float4 xa = s_x[lane + 64 * j], w = s_wr[wv][lane + 64 * j];
+                        const float4 xa = s_x[lane + 64 * j], w = s_wr[lw][lane + 64 * j];
                         s += w.x * xa.x + w.y * xa.y + w.z * xa.z + w.w * xa.w;
                     }
                     s = group_sum<64>(s);
@@ -580,7 +624,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 }
 #pragma unroll
                 for (int k = 0; k < NBE / 2; k++) {
-                    const int blk = wv * (NBE / 2) + k;
+                    const int blk = lw * (NBE / 2) + k;
                     const Q8Lane q = q8k_quant_lane(s_x[blk * 64 + lane]);
                     ((uint32_t *)s_xrec)[blk * 64 + lane] = q.packed;
                     if ((lane & 3) == 0) ((int *)s_xrec)[XR_S + blk * 16 + (lane >> 2)] = q.gsum;
@@ -632,7 +676,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                     if (tid < 8 * S + NBE / 2) return 4 * ((TW_XQ + rep * XR_WORDS + XR_G) / 2 + tid - 8 * S) + 3;
                     return -1;
                 };
-                ok = pollq<1>(rs, 0, yp, seq, v, abort_flag);
+                ok = pollq<1>(rs, 0, yp, seq, v, ab);
                 if (tid < 8 * S) {
                     s_dres[2 * (tid & 7)][tid >> 3] = __uint_as_float(v[0][0]);
                     s_dres[2 * (tid & 7) + 1][tid >> 3] = __uint_as_float(v[0][1]);
@@ -704,7 +748,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             if (wv == 0) {
                 uint32_t g1[1];
                 ok = poll<1>(tg->logits[rep], [&](int) { return lane == 0 ? logit_pos((b * 37) % E) : -1; }, seq, g1,
-                             abort_flag);
+                             ab);
                 float lg[4];
                 ok = ok && read_logits(E, seq, lg);
                 TR(7);
@@ -715,7 +759,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 TR(6);
             } else if (wv >= 2) {
                 uint32_t g1[1];
-                ok = poll<1>(tg->xq[rep], [&](int) { return lane == 0 ? XR_G + (b & 7) : -1; }, seq, g1, abort_flag);
+                ok = poll<1>(tg->xq[rep], [&](int) { return lane == 0 ? XR_G + (b & 7) : -1; }, seq, g1, ab);
                 if (sh_row < F) gu_load(sh_h, sh_0, sh_1, (const uint8_t *)(half ? L.up_shexp : L.gate_shexp), sh_row);
                 constexpr int XP = (XR_WORDS / 2 + 63) / 64;   // 6 word pairs per lane
                 uint32_t v[XP][2];
@@ -723,7 +767,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                     const int p = lane + 64 * k;       // word pair (the whole record is written)
                     return p < XR_WORDS / 2 ? 4 * p + 3 : -1;
                 };
-                ok = ok && pollq<XP>(rs, TW_XQ + rep * XR_WORDS, xp, seq, v, abort_flag);
+                ok = ok && pollq<XP>(rs, TW_XQ + rep * XR_WORDS, xp, seq, v, ab);
 #pragma unroll
                 for (int k = 0; k < XP; k++)
                     if (xp(k) >= 0) ((uint2 *)s_xrec)[xp(k) >> 2] = make_uint2(v[k][0], v[k][1]);
@@ -734,7 +778,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                     if (lane == 0) st64(rs, TW_H + K * F + sh_row, __float_as_uint(hv), seq);
                 }
             }
-            if (!wg_all(ok, s_vote, 1)) return;
+            if (!wg_all(ok && !(l == 0 && pre_abort), s_vote, 1)) return;
             TR(2);
             // the shared registers count as read on every path from here on,
             // so no later write into them has to wait for the load queue
@@ -755,10 +799,10 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                     if (wv == 0) {                    // one word first, as for x
                         uint32_t g1[1];
                         ok = poll<1>(tg->h + dslot * F, [&](int) { return lane == 0 ? F - 1 - (b % 64) : -1; }, seq, g1,
-                                     abort_flag);
+                                     ab);
                     }
                     if (!wg_all(ok, s_vote, 0)) return;
-                    ok = pollq<1>(rs, TW_H + dslot * F, [&](int) { return 4 * tid + 3; }, seq, v, abort_flag);
+                    ok = pollq<1>(rs, TW_H + dslot * F, [&](int) { return 4 * tid + 3; }, seq, v, ab);
                     ((float2 *)s_hs)[tid] = make_float2(__uint_as_float(v[0][0]), __uint_as_float(v[0][1]));
                 }
                 if (!wg_all(ok, s_vote, 3)) return;
@@ -821,6 +865,13 @@ bool fused_eligible(const qmag_moe_layer *L, int n_layer)
         if (a.n_embd != fused::N || a.n_ff != fused::F || a.n_expert < 1 || a.n_expert > 256 ||
             a.n_used < 1 || a.n_used > 8 || a.n_used > a.n_expert)
             return false;
+        // One tagged slot per buffer is safe only if every workgroup that
+        // reads a layer's words lies on that layer's dependency chain; with
+        // n_used >= 4 every wave has a routed gate/up row pair, so it does.
+        // With fewer, some workgroups read the logits and feed nothing, and
+        // in a multi-layer launch the next layer could overwrite the words
+        // before they read them.  One-layer launches are safe for any n_used.
+        if (n_layer > 1 && a.n_used < 4) return false;
         if (a.t_down_exps != a.t_down_shexp || a.t_down_exps != L[0].t_down_exps) return false;
     }
     if (g_coop_ok < 0) {
@@ -845,18 +896,84 @@ static int rearm()
     return QMAG_OK;
 }
 
-int fused_status()
+static bool g_pending = false;       // a launch was issued since the last fused_status()
+bool fused_pending() { return g_pending; }
+
+// Recovery log: the calls issued since the last status check.  If a wait
+// of launch e expired, launch e left its output partly written and every
+// later launch exited at its first barrier without writing any; the calls
+// are then re-run from launch e on through the launch sequence, in-place
+// calls first restored from the copy of their input taken before they ran.
+struct FusedCall {
+    std::vector<qmag_moe_layer> layers;
+    float *x = nullptr, *out = nullptr;   // out == nullptr: the stack (x updated in place)
+    int n_tok = 0;
+    unsigned first_epoch = 0;             // epoch of the call's first launch (token 0)
+    int snap = -1;                        // snapshot slot holding the input rows, or -1
+};
+// At most LOG_CALLS calls, SNAP_SLOTS of them in place, between status
+// checks; a call that would exceed either first checks (a stream sync).
+constexpr int LOG_CALLS = 1024, SNAP_SLOTS = 8;
+static std::vector<FusedCall> g_log;
+static int g_snap_used = 0;
+static float *g_snap[SNAP_SLOTS] = {};
+static size_t g_snap_bytes[SNAP_SLOTS] = {};
+static long g_recovered = 0;
+static int g_test_abort = 0;
+
+static int replay(const std::vector<FusedCall> &log, unsigned e, hipStream_t s)
 {
-    if (!g_abort) return QMAG_OK;
-    int abort_flag = 0;
-    QMAG_HIP(hipMemcpy(&abort_flag, g_abort, sizeof(int), hipMemcpyDeviceToHost));
-    if (abort_flag) {
-        int st = rearm();
-        if (st) return st;
-        return fail(QMAG_ERR_KERNEL, "fused MoE decode: a cross-workgroup wait hit its spin limit");
+    const size_t N = fused::N;
+    for (const FusedCall &c : log) {
+        if (c.first_epoch + (unsigned)c.n_tok <= e) continue;         // finished before launch e
+        const int t0 = e > c.first_epoch ? (int)(e - c.first_epoch) : 0;
+        const size_t rows = (size_t)(c.n_tok - t0) * N;
+        if (c.snap >= 0)
+            QMAG_HIP(hipMemcpyAsync(c.x + t0 * N, g_snap[c.snap] + t0 * N, sizeof(float) * rows,
+                                    hipMemcpyDeviceToDevice, s));
+        for (int t = t0; t < c.n_tok; t++) {
+            float *xt = c.x + t * N;
+            if (!c.out) {
+                for (const qmag_moe_layer &L : c.layers) {
+                    int st = moe_ffn(&L, xt, xt, 1, xt, s);
+                    if (st) return st;
+                }
+            } else {
+                int st = moe_ffn(&c.layers[0], xt, c.out + t * N, 1, nullptr, s);
+                if (st) return st;
+            }
+        }
     }
+    moe_note_sequence_ran();
+    QMAG_HIP(hipStreamSynchronize(s));
     return QMAG_OK;
 }
+
+int fused_status()
+{
+    g_pending = false;
+    if (!g_abort) {
+        g_log.clear();
+        g_snap_used = 0;
+        return QMAG_OK;
+    }
+    QMAG_HIP(hipStreamSynchronize(ctx().stream));
+    int word = 0;
+    QMAG_HIP(hipMemcpy(&word, g_abort, sizeof(int), hipMemcpyDeviceToHost));
+    std::vector<FusedCall> log;
+    log.swap(g_log);
+    g_snap_used = 0;
+    if (word == 0) return QMAG_OK;
+    int st = rearm();
+    if (st) return st;
+    st = replay(log, (unsigned)word - 1u, ctx().stream);
+    if (st) return st;
+    g_recovered++;
+    return QMAG_OK;
+}
+
+long fused_recoveries() { return g_recovered; }
+void fused_test_abort_next(int nth) { g_test_abort = nth > 0 ? nth : 0; }
 
 static uint32_t layer_hash(const qmag_moe_layer *L)
 {
@@ -918,10 +1035,6 @@ static int fused_prepare(const qmag_moe_layer *L, int n_layer, hipStream_t s, co
         }
         *dl = g_dev_layers;
     }
-    if (g_epoch >= (1u << 24)) {           // tags would wrap: zero the buffers, restart
-        int st = rearm();
-        if (st) return st;
-    }
     if (option(QMAG_OPT_TRACE)) {
         const size_t need = sizeof(unsigned long long) * fused::WGS * (size_t)n_layer * 8;
         if (need > g_trace_bytes) {
@@ -941,13 +1054,16 @@ static int fused_prepare(const qmag_moe_layer *L, int n_layer, hipStream_t s, co
     return QMAG_OK;
 }
 
-int fused_launch(const qmag_moe_layer *L, int n_layer, float *x, float *out, hipStream_t s)
+static int fused_launch(const qmag_moe_layer *L, const qmag_moe_layer *dl, int n_layer, float *x, float *out,
+                        hipStream_t s)
 {
-    if (out && n_layer != 1) return fail(QMAG_ERR_ARG, "fused: out mode needs exactly one layer");
-    const qmag_moe_layer *dl = nullptr;
-    int st = fused_prepare(L, n_layer, s, &dl);
-    if (st) return st;
     unsigned epoch = g_epoch;
+    if (g_test_abort > 0 && --g_test_abort == 0) {   // test hook: this launch finds the abort word set
+        static int code;
+        code = (int)epoch + 1;
+        QMAG_HIP(hipMemcpyAsync(g_abort, &code, sizeof(int), hipMemcpyHostToDevice, s));
+        QMAG_HIP(hipStreamSynchronize(s));
+    }
     unsigned long long *trace = option(QMAG_OPT_TRACE) ? g_trace : nullptr;
     void *args[] = {(void *)&dl,      (void *)&n_layer, (void *)&x,     (void *)&out,
                     (void *)&g_tagged, (void *)&g_logits, (void *)&g_h, (void *)&g_sel,
@@ -963,6 +1079,52 @@ int fused_launch(const qmag_moe_layer *L, int n_layer, float *x, float *out, hip
         QMAG_HIP(hipLaunchKernel(k, dim3(fused::WGS), dim3(256), args, 0, s));
     prof_end(PROF_FUSED, s);
     g_epoch++;
+    g_pending = true;
+    return QMAG_OK;
+}
+
+int fused_call(const qmag_moe_layer *L, int n_layer, float *x, float *out, int n_tok, hipStream_t s)
+{
+    if (out && n_layer != 1) return fail(QMAG_ERR_ARG, "fused: out mode needs exactly one layer");
+    if (n_tok <= 0 || n_tok >= (1 << 23)) return fail(QMAG_ERR_ARG, "fused: n_tok=%d", n_tok);
+    const bool wraps = g_epoch + (unsigned)n_tok >= (1u << 24);     // tags would wrap
+    const bool in_place = !out || out == x;
+    if (g_log.size() >= (size_t)LOG_CALLS || (in_place && g_snap_used == SNAP_SLOTS) || wraps) {
+        int st = fused_status();
+        if (st) return st;
+        if (wraps) {
+            st = rearm();
+            if (st) return st;
+        }
+    }
+    const qmag_moe_layer *dl = nullptr;
+    int st = fused_prepare(L, n_layer, s, &dl);
+    if (st) return st;
+    FusedCall c;
+    c.layers.assign(L, L + n_layer);
+    c.x = x;
+    c.out = out;
+    c.n_tok = n_tok;
+    c.first_epoch = g_epoch;
+    if (in_place) {                     // keep the input to replay from
+        const int slot = g_snap_used++;
+        const size_t need = sizeof(float) * fused::N * (size_t)n_tok;
+        if (need > g_snap_bytes[slot]) {
+            QMAG_HIP(hipStreamSynchronize(s));
+            if (g_snap[slot]) QMAG_HIP(hipFree(g_snap[slot]));
+            g_snap[slot] = nullptr;
+            g_snap_bytes[slot] = 0;
+            QMAG_HIP(hipMalloc(&g_snap[slot], need));
+            g_snap_bytes[slot] = need;
+        }
+        QMAG_HIP(hipMemcpyAsync(g_snap[slot], x, need, hipMemcpyDeviceToDevice, s));
+        c.snap = slot;
+    }
+    g_log.push_back(std::move(c));
+    for (int t = 0; t < n_tok; t++) {
+        st = fused_launch(L, dl, n_layer, x + (size_t)t * fused::N, out ? out + (size_t)t * fused::N : nullptr, s);
+        if (st) return st;
+    }
     return QMAG_OK;
 }
 

@@ -5,13 +5,17 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/qma_gpu.h"
 #include "qmag_device.h"
 
 namespace qmag {
 
 struct Ctx {
-    bool ready = false;
+    // set (release) once the fields below are filled in; read with acquire
+    // by every entry point, from any thread
+    std::atomic<bool> ready{false};
     int dev = -1;
     hipStream_t stream = nullptr;
     hipEvent_t ev[64] = {};
@@ -63,8 +67,14 @@ int launch_q8k_quant(const float *x, int nblocks, int8_t *xq, float *xd, int16_t
                      hipStream_t s);
 int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
                   int n_in, int n_out, int T, int wtype, float *out, hipStream_t s);
-// T = 1 with x in f32: the matvec quantises x to Q8_K itself (bit-identical)
+// T = 1 with x in f32: the matvec quantises x to Q8_K itself (bit-identical);
+// available for the row lengths matvec_x_supported() accepts
+bool matvec_x_supported(int n_in);
 int launch_matvec_x(const float *x, const void *W, int n_in, int n_out, int wtype, float *out, hipStream_t s);
+// fp32 path of quants.c (qmag_quants.hip)
+int launch_dequant(const void *W, int wtype, long n, float *y, hipStream_t s);
+int launch_f32dot(const float *x, const void *W, int n_in, int n_out, int T, int wtype, float *out,
+                  hipStream_t s);
 int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const float *resid,
             hipStream_t s);
 int moe_check_layer(const qmag_moe_layer *L);
@@ -77,8 +87,16 @@ int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, 
 
 // persistent single-launch decode (qmag_fused.hip)
 bool fused_eligible(const qmag_moe_layer *L, int n_layer);
-int fused_launch(const qmag_moe_layer *L, int n_layer, float *x, float *out, hipStream_t s);
+// n_tok tokens through n_layer layers, one launch per token: x (and out,
+// when not null: one layer, out = moe(x)) are [n_tok][2048]
+int fused_call(const qmag_moe_layer *L, int n_layer, float *x, float *out, int n_tok, hipStream_t s);
+long fused_recoveries();
+void fused_test_abort_next(int nth);
+// the launch sequence wrote the latest stage outputs (qmag_moe_last_stage)
+void moe_note_sequence_ran();
 int fused_status();
+// true when a persistent decode launch was issued since the last status check
+bool fused_pending();
 int fused_trace_read(void *dst, size_t bytes);
 int fused_last_stage(const float **logits, const int **sel, const float **w, const float **gs,
                      const float **h);

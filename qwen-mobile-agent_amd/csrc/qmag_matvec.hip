@@ -208,10 +208,66 @@ static int launch_mv_nb(const int8_t *xq, const float *xd, const int16_t *xsum, 
     return QMAG_OK;
 }
 
+// Any row length (nb super-blocks, not only the powers of two the tiled
+// kernel is instantiated for): one wave per row, lane l taking tasks
+// l, l + 64, ... of the row (4 per super-block, so the 4 tasks of a Q6_K
+// block stay in one lane quad for its exact integer block sum).
+template <int WT>
+__global__ __launch_bounds__(256) void matvec_any_kernel(const uint8_t *__restrict__ W,
+                                                         const int8_t *__restrict__ xq,
+                                                         const float *__restrict__ xd,
+                                                         const int16_t *__restrict__ xsum,
+                                                         float *__restrict__ out, int nb, int n_out, int T)
+{
+    using RT = RowTask<WT>;
+    const int lane = lane_id(), q = lane & 3;
+    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nwave = (int)((gridDim.x * blockDim.x) >> 6);
+    const size_t rb = (size_t)nb * RT::BLOCK;
+    const int ntask = 4 * nb, n_in = nb * QK_K;
+    for (int row = wave; row < n_out; row += nwave) {
+        for (int t = 0; t < T; t++) {
+            float v = 0.0f;
+            for (int tk = lane; tk < ntask; tk += 64) {
+                typename RT::Raw r;
+                typename RT::Act a;
+                RT::load_raw(r, W + (size_t)row * rb + (size_t)(tk >> 2) * RT::BLOCK, q);
+                RT::load_act(a, xq + (size_t)t * n_in, xd + (size_t)t * nb, xsum + (size_t)t * (n_in / 16),
+                             tk >> 2, q);
+                v += RT::dot(r, a, q);
+            }
+            v = group_sum<64>(v);
+            if (lane == 0) out[(size_t)t * n_out + row] = v;
+        }
+    }
+}
+
+template <int WT>
+static int launch_mv_any(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W, int nb,
+                         int n_out, int T, float *out, hipStream_t s)
+{
+    const long cap = (long)(ctx().n_cu > 0 ? ctx().n_cu : 256) * 32;    // waves
+    const long waves = n_out < cap ? n_out : cap;
+    const int wgs = (int)((waves + 3) / 4);
+    prof_begin(PROF_MATVEC, s);
+    hipLaunchKernelGGL(matvec_any_kernel<WT>, dim3(wgs), dim3(256), 0, s, (const uint8_t *)W, xq, xd, xsum, out,
+                       nb, n_out, T);
+    prof_end(PROF_MATVEC, s);
+    QMAG_HIP(hipGetLastError());
+    return QMAG_OK;
+}
+
+// the tiled kernel is instantiated for these row lengths (super-blocks)
+static bool tiled_nb(int nb) { return nb == 1 || nb == 2 || nb == 4 || nb == 8 || nb == 16 || nb == 32; }
+
 template <int WT>
 static int launch_mv_t(const int8_t *xq, const float *xd, const int16_t *xsum, const void *W,
                        int n_in, int n_out, int T, float *out, hipStream_t s, const float *xf)
 {
+    if (!tiled_nb(n_in / QK_K)) {
+        if (xf) return fail(QMAG_ERR_ARG, "matvec: internal: fused Q8_K path needs a tiled row length");
+        return launch_mv_any<WT>(xq, xd, xsum, W, n_in / QK_K, n_out, T, out, s);
+    }
     switch (n_in / QK_K) {
     case 1: return launch_mv_nb<WT, 1>(xq, xd, xsum, W, n_out, T, out, s, xf);
     case 2: return launch_mv_nb<WT, 2>(xq, xd, xsum, W, n_out, T, out, s, xf);
@@ -219,7 +275,7 @@ static int launch_mv_t(const int8_t *xq, const float *xd, const int16_t *xsum, c
     case 8: return launch_mv_nb<WT, 8>(xq, xd, xsum, W, n_out, T, out, s, xf);
     case 16: return launch_mv_nb<WT, 16>(xq, xd, xsum, W, n_out, T, out, s, xf);
     case 32: return launch_mv_nb<WT, 32>(xq, xd, xsum, W, n_out, T, out, s, xf);
-    default: return fail(QMAG_ERR_ARG, "matvec: n_in=%d not in {256..8192} powers of two", n_in);
+    default: return fail(QMAG_ERR_ARG, "matvec: internal: n_in=%d has no tiled instance", n_in);
     }
 }
 
@@ -235,9 +291,12 @@ int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const 
     return fail(QMAG_ERR_ARG, "matvec: unsupported wtype %d", wtype);
 }
 
+bool matvec_x_supported(int n_in) { return n_in > 0 && n_in % QK_K == 0 && tiled_nb(n_in / QK_K); }
+
 int launch_matvec_x(const float *x, const void *W, int n_in, int n_out, int wtype, float *out, hipStream_t s)
 {
     if (n_in <= 0 || n_in % QK_K || n_out <= 0) return fail(QMAG_ERR_ARG, "matvec: n_in=%d n_out=%d", n_in, n_out);
+    if (!matvec_x_supported(n_in)) return fail(QMAG_ERR_ARG, "matvec: internal: n_in=%d has no fused Q8_K form", n_in);
     if (!x || !W || !out) return fail(QMAG_ERR_ARG, "matvec: null pointer");
     if (wtype == QMAG_TYPE_Q4_K)
         return launch_mv_t<QMAG_TYPE_Q4_K>(nullptr, nullptr, nullptr, W, n_in, n_out, 1, out, s, x);

@@ -522,7 +522,7 @@ extern "C" int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *
     if (T == 1 && option(QMAG_OPT_FUSED) && fused_eligible(L, 1)) {
         if (!x || !out) return fail(QMAG_ERR_ARG, "moe: null x/out");
         g_last_fused = true;
-        return fused_launch(L, 1, (float *)x, out, ctx().stream);
+        return fused_call(L, 1, (float *)x, out, 1, ctx().stream);
     }
     g_last_fused = false;
     return moe_ffn(L, x, out, T, nullptr, ctx().stream);
@@ -541,11 +541,7 @@ extern "C" int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, flo
     const int N = layers[0].n_embd;
     if (option(QMAG_OPT_FUSED) && fused_eligible(layers, n_layer)) {
         g_last_fused = true;
-        for (int t = 0; t < n_tok; t++) {
-            st = fused_launch(layers, n_layer, x + (size_t)t * N, nullptr, ctx().stream);
-            if (st) return st;
-        }
-        return QMAG_OK;
+        return fused_call(layers, n_layer, x, nullptr, n_tok, ctx().stream);
     }
     g_last_fused = false;
     for (int t = 0; t < n_tok; t++) {
@@ -557,6 +553,10 @@ extern "C" int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, flo
     }
     return QMAG_OK;
 }
+
+namespace qmag {
+void moe_note_sequence_ran() { g_last_fused = false; }
+}  // namespace qmag
 
 extern "C" int qmag_moe_last_stage(const float **logits, const int **sel, const float **w,
                                    const float **gs, const float **h)

@@ -1,0 +1,222 @@
+// qmag_quants.hip -- the fp32 half of the k-quant path (src/quants.c):
+// Q4_K / Q6_K dequantisation (quants.c:29-75, the closed-form weight
+// definition, also what embed_row uses, nn.c:2044-2054) and the
+// dequantise-then-dot fp32 matvec (quants.c:80-133; the QMA_NOQ8K path of
+// moe_expert_one / moe_shared, nn.c:393-407, 475-492).
+//
+// Both are HBM-bound streams over the GGUF block bytes.  Dequantisation is
+// bit-identical to the reference's unfused fp32 form: w = d1*q - m1 with
+// d1 = d*sc and m1 = dmin*m rounded separately (Q4_K), w = (d*sc)*q (Q6_K);
+// the multiplies and the subtraction are issued as separately rounded
+// operations so the compiler cannot contract them into an FMA.
+#include "qmag_internal.h"
+
+namespace qmag {
+
+// ------------------------------------------------------------ dequant ----
+// One wave per 256-value super-block; lane l writes elements 4l..4l+3.
+template <int WT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict__ W, long nblocks,
+                                                      float *__restrict__ y)
+{
+    const long blk = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (blk >= nblocks) return;                 // wave-uniform
+    const int lane = lane_id();
+    const int e0 = 4 * lane;
+    float4 o;
+    if constexpr (WT == QMAG_TYPE_Q4_K) {
+        const uint8_t *b = W + blk * Q4K_BYTES;
+        const uint4 hdr = ld16(b);
+        const int j = e0 >> 5;                  // sub-block 0..7
+        const int g = j >> 1;                   // 64-value group: bytes qs[32g..32g+31]
+        const uint32_t qw = ld4(b + 16 + 32 * g + (e0 & 31));
+        uint32_t sc, m;
+        q4_scale_min(j, hdr.y, hdr.z, hdr.w, sc, m);
+        const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
+        const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)m);
+        const uint32_t nib = (j & 1) ? (qw >> 4) & 0x0F0F0F0Fu : qw & 0x0F0F0F0Fu;
+        o.x = __fsub_rn(__fmul_rn(d1, (float)(nib & 255)), m1);
+        o.y = __fsub_rn(__fmul_rn(d1, (float)((nib >> 8) & 255)), m1);
+        o.z = __fsub_rn(__fmul_rn(d1, (float)((nib >> 16) & 255)), m1);
+        o.w = __fsub_rn(__fmul_rn(d1, (float)(nib >> 24)), m1);
+    } else {
+        const uint8_t *b = W + blk * Q6K_BYTES;
+        const int n = e0 >> 7, r = e0 & 127, Q = r >> 5, l = r & 31;
+        const uint32_t lw = ld4(b + 64 * n + 32 * (Q & 1) + l);
+        const uint32_t hw = ld4(b + 128 + 32 * n + l);
+        const int sc = (int)(int8_t)b[192 + 8 * n + (l >> 4) + 2 * Q];
+        const float d = h2f(ld2(b + 208));
+        const float ds = __fmul_rn(d, (float)sc);
+        const uint32_t lo = (Q >= 2 ? lw >> 4 : lw) & 0x0F0F0F0Fu;
+        const uint32_t hi = (hw >> (2 * Q)) & 0x03030303u;
+        const uint32_t q = lo | (hi << 4);
+        o.x = __fmul_rn(ds, (float)((int)(q & 255) - 32));
+        o.y = __fmul_rn(ds, (float)((int)((q >> 8) & 255) - 32));
+        o.z = __fmul_rn(ds, (float)((int)((q >> 16) & 255) - 32));
+        o.w = __fmul_rn(ds, (float)((int)(q >> 24) - 32));
+    }
+    ((float4 *)(y + blk * QK_K))[lane] = o;
+}
+
+int launch_dequant(const void *W, int wtype, long n, float *y, hipStream_t s)
+{
+    if (n <= 0 || n % QK_K) return fail(QMAG_ERR_ARG, "dequant: n=%ld is not a positive multiple of 256", n);
+    if (!W || !y) return fail(QMAG_ERR_ARG, "dequant: null pointer");
+    const long nb = n / QK_K;
+    const long wgs = (nb + 3) / 4;
+    if (wtype == QMAG_TYPE_Q4_K)
+        hipLaunchKernelGGL(dequant_kernel<QMAG_TYPE_Q4_K>, dim3((unsigned)wgs), dim3(256), 0, s,
+                           (const uint8_t *)W, nb, y);
+    else if (wtype == QMAG_TYPE_Q6_K)
+        hipLaunchKernelGGL(dequant_kernel<QMAG_TYPE_Q6_K>, dim3((unsigned)wgs), dim3(256), 0, s,
+                           (const uint8_t *)W, nb, y);
+    else
+        return fail(QMAG_ERR_ARG, "dequant: unsupported wtype %d", wtype);
+    QMAG_HIP(hipGetLastError());
+    return QMAG_OK;
+}
+
+// ------------------------------------------------------ fp32 matvec ----
+// out[t][r] = sum_i deq(W[r])_i * x[t][i].  x of one token sits in LDS; a row
+// is split into 64-value tasks (Q4_K: one nibble group of a super-block, the
+// 16-byte header and 32 bytes of nibbles; Q6_K: a quarter block) spread over
+// LPR lanes, each lane looping over its tasks.  Grid: (row chunks, T).
+constexpr int F32_MAX_IN = 8192;
+
+template <int WT>
+__device__ __forceinline__ float f32_task(const uint8_t *row, int t, const float *xs)
+{
+    const int ib = t >> 2, q = t & 3;
+    if constexpr (WT == QMAG_TYPE_Q4_K) {
+        const uint8_t *b = row + (size_t)ib * Q4K_BYTES;
+        const uint4 hdr = ld16(b), q0 = ld16(b + 16 + 32 * q), q1 = ld16(b + 32 + 32 * q);
+        const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
+        uint32_t s1, m1, s2, m2;
+        q4_scale_min(2 * q, hdr.y, hdr.z, hdr.w, s1, m1);
+        q4_scale_min(2 * q + 1, hdr.y, hdr.z, hdr.w, s2, m2);
+        const float d1 = d * (float)s1, dm1 = dmin * (float)m1;
+        const float d2 = d * (float)s2, dm2 = dmin * (float)m2;
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const float4 *xv = (const float4 *)(xs + ib * QK_K + 64 * q);
+        float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 a = xv[k], c = xv[8 + k];
+            const uint32_t w = qw[k];
+            lo += (d1 * (float)(w & 15) - dm1) * a.x + (d1 * (float)((w >> 8) & 15) - dm1) * a.y +
+                  (d1 * (float)((w >> 16) & 15) - dm1) * a.z + (d1 * (float)((w >> 24) & 15) - dm1) * a.w;
+            hi += (d2 * (float)((w >> 4) & 15) - dm2) * c.x + (d2 * (float)((w >> 12) & 15) - dm2) * c.y +
+                  (d2 * (float)((w >> 20) & 15) - dm2) * c.z + (d2 * (float)((w >> 28) & 15) - dm2) * c.w;
+        }
+        return lo + hi;
+    } else {
+        const uint8_t *b = row + (size_t)ib * Q6K_BYTES;
+        const int n = q >> 1, l16 = q & 1;
+        Q6Raw r;
+        q6_load_raw(r, b, n, l16);
+        const float d = h2f(r.d);
+        const uint64_t sc8 = ((uint64_t)r.sc.y << 32) | r.sc.x;
+        const uint32_t L[4] = {r.ql_lo.x, r.ql_lo.y, r.ql_lo.z, r.ql_lo.w};
+        const uint32_t H[4] = {r.ql_hi.x, r.ql_hi.y, r.ql_hi.z, r.ql_hi.w};
+        const uint32_t B[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        float acc = 0.0f;
+#pragma unroll
+        for (int Q = 0; Q < 4; Q++) {
+            const float ds = d * (float)(int)(int8_t)((sc8 >> (8 * (l16 + 2 * Q))) & 255);
+            const float4 *xv = (const float4 *)(xs + ib * QK_K + 128 * n + 32 * Q + 16 * l16);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t src = (Q & 1) ? H[k] : L[k];
+                const uint32_t lo = (Q >= 2 ? src >> 4 : src) & 0x0F0F0F0Fu;
+                const uint32_t qv = lo | (((B[k] >> (2 * Q)) & 0x03030303u) << 4);
+                const float4 a = xv[k];
+                acc += ds * (float)((int)(qv & 255) - 32) * a.x + ds * (float)((int)((qv >> 8) & 255) - 32) * a.y +
+                       ds * (float)((int)((qv >> 16) & 255) - 32) * a.z + ds * (float)((int)(qv >> 24) - 32) * a.w;
+            }
+        }
+        return acc;
+    }
+}
+
+template <int WT, int LPR>
+__global__ __launch_bounds__(256) void f32dot_kernel(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                                     float *__restrict__ out, int nb, int n_out)
+{
+    __shared__ __align__(16) float s_x[F32_MAX_IN];
+    const int t = (int)blockIdx.y;
+    const int n_in = nb * QK_K;
+    const float *xt = x + (size_t)t * n_in;
+    for (int i = (int)threadIdx.x; i < n_in / 4; i += (int)blockDim.x)
+        ((float4 *)s_x)[i] = ldg4(xt + 4 * i);
+    __syncthreads();
+    const size_t rb = (size_t)nb * (WT == QMAG_TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES);
+    const int lane = lane_id(), sub = lane % LPR;
+    const int rows_per_wave = 64 / LPR;
+    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nwave = (int)((gridDim.x * blockDim.x) >> 6);
+    const int ntask = 4 * nb;
+    for (int base = wave * rows_per_wave; base < n_out; base += nwave * rows_per_wave) {
+        const int row = base + lane / LPR;
+        float v = 0.0f;
+        if (row < n_out)
+            for (int tk = sub; tk < ntask; tk += LPR) v += f32_task<WT>(W + (size_t)row * rb, tk, s_x);
+        v = group_sum<LPR>(v);
+        if (sub == 0 && row < n_out) out[(size_t)t * n_out + row] = v;
+    }
+}
+
+template <int WT>
+static int launch_f32dot_t(const float *x, const void *W, int nb, int n_out, int T, float *out, hipStream_t s)
+{
+    const int ntask = 4 * nb;
+    const int lpr = ntask >= 64 ? 64 : ntask > 16 ? 32 : ntask > 8 ? 16 : ntask > 4 ? 8 : 4;
+    const long rows_per_wg = 4L * (64 / lpr);
+    long wgs = ((long)n_out + rows_per_wg - 1) / rows_per_wg;
+    const long cap = (long)(ctx().n_cu > 0 ? ctx().n_cu : 256) * 8 / (T < 8 ? T : 8);
+    if (wgs > cap) wgs = cap;
+    const dim3 grid((unsigned)wgs, (unsigned)T);
+    const uint8_t *w = (const uint8_t *)W;
+    switch (lpr) {
+    case 4: hipLaunchKernelGGL((f32dot_kernel<WT, 4>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
+    case 8: hipLaunchKernelGGL((f32dot_kernel<WT, 8>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
+    case 16: hipLaunchKernelGGL((f32dot_kernel<WT, 16>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
+    case 32: hipLaunchKernelGGL((f32dot_kernel<WT, 32>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
+    default: hipLaunchKernelGGL((f32dot_kernel<WT, 64>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
+    }
+    QMAG_HIP(hipGetLastError());
+    return QMAG_OK;
+}
+
+int launch_f32dot(const float *x, const void *W, int n_in, int n_out, int T, int wtype, float *out,
+                  hipStream_t s)
+{
+    if (n_in <= 0 || n_in % QK_K || n_in > F32_MAX_IN || n_out <= 0 || T <= 0 || T > 65535)
+        return fail(QMAG_ERR_ARG, "f32 matvec: n_in=%d (multiple of 256, <= %d) n_out=%d T=%d", n_in,
+                    F32_MAX_IN, n_out, T);
+    if (!x || !W || !out) return fail(QMAG_ERR_ARG, "f32 matvec: null pointer");
+    if (wtype == QMAG_TYPE_Q4_K) return launch_f32dot_t<QMAG_TYPE_Q4_K>(x, W, n_in / QK_K, n_out, T, out, s);
+    if (wtype == QMAG_TYPE_Q6_K) return launch_f32dot_t<QMAG_TYPE_Q6_K>(x, W, n_in / QK_K, n_out, T, out, s);
+    return fail(QMAG_ERR_ARG, "f32 matvec: unsupported wtype %d", wtype);
+}
+
+}  // namespace qmag
+
+using namespace qmag;
+
+extern "C" {
+
+int qmag_dequant_dev(const void *W, int wtype, int64_t n, float *y)
+{
+    int st = require_ready();
+    if (st) return st;
+    return launch_dequant(W, wtype, (long)n, y, ctx().stream);
+}
+
+int qmag_matmul_f32_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype, float *out)
+{
+    int st = require_ready();
+    if (st) return st;
+    return launch_f32dot(x, W, n_in, n_out, T, wtype, out, ctx().stream);
+}
+
+}  // extern "C"

@@ -49,7 +49,7 @@ int hip_fail(hipError_t e, const char *what, const char *file, int line)
 
 int require_ready()
 {
-    if (!g_ctx.ready) return fail(QMAG_ERR_NODEV, "qmag_init() has not succeeded");
+    if (!g_ctx.ready.load(std::memory_order_acquire)) return fail(QMAG_ERR_NODEV, "qmag_init() has not succeeded");
     return QMAG_OK;
 }
 
@@ -106,16 +106,19 @@ static hipEvent_t prof_event()
     return e;
 }
 
+// Only launches on the library stream are timed: the reference-compatible
+// entries run on per-thread streams from concurrent host threads and are
+// never bracketed (the records below are not shared-state safe).
 void prof_begin(int id, hipStream_t s)
 {
-    if (!g_prof) return;
+    if (!g_prof || s != g_ctx.stream) return;
     hipEvent_t e = prof_event();
     if (e && hipEventRecord(e, s) == hipSuccess) g_prof_open[id] = e;
 }
 
 void prof_end(int id, hipStream_t s)
 {
-    if (!g_prof || !g_prof_open[id]) return;
+    if (!g_prof || s != g_ctx.stream || !g_prof_open[id]) return;
     hipEvent_t e = prof_event();
     if (e && hipEventRecord(e, s) == hipSuccess) g_prof_recs.push_back({id, g_prof_open[id], e});
     g_prof_open[id] = nullptr;
@@ -175,7 +178,8 @@ const char *qmag_last_error(void) { return t_err; }
 int qmag_init(int device)
 {
     std::lock_guard<std::mutex> lk(g_mu);
-    if (g_ctx.ready) return g_ctx.dev == device ? QMAG_OK : fail(QMAG_ERR_ARG, "already initialised on device %d", g_ctx.dev);
+    if (g_ctx.ready.load(std::memory_order_acquire))
+        return g_ctx.dev == device ? QMAG_OK : fail(QMAG_ERR_ARG, "already initialised on device %d", g_ctx.dev);
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n <= device || device < 0)
@@ -194,7 +198,7 @@ int qmag_init(int device)
     g_ctx.clock_khz = prop.clockRate;
     g_ctx.hbm = prop.totalGlobalMem;
     snprintf(g_ctx.arch, sizeof(g_ctx.arch), "%s", prop.gcnArchName);
-    g_ctx.ready = true;
+    g_ctx.ready.store(true, std::memory_order_release);
     return QMAG_OK;
 }
 
@@ -239,6 +243,13 @@ int qmag_d2h(void *dst, const void *src, size_t bytes)
 {
     int st = require_ready();
     if (st) return st;
+    // results read back after persistent decode launches are only good if
+    // none of their bounded waits expired: check first (as qmag_sync does),
+    // which re-runs the affected calls through the launch sequence if one did
+    if (fused_pending()) {
+        st = fused_status();
+        if (st) return st;
+    }
     QMAG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.stream));
     QMAG_HIP(hipStreamSynchronize(g_ctx.stream));
     return QMAG_OK;
@@ -286,7 +297,18 @@ int qmag_set_option(int opt, int value)
         g_opt_grouped = value != 0;
         return QMAG_OK;
     }
+    if (opt == QMAG_OPT_TEST_ABORT) {
+        fused_test_abort_next(value);
+        return QMAG_OK;
+    }
     return fail(QMAG_ERR_ARG, "unknown option %d", opt);
+}
+
+int qmag_fused_recoveries(long *count)
+{
+    if (!count) return fail(QMAG_ERR_ARG, "null count");
+    *count = fused_recoveries();
+    return QMAG_OK;
 }
 
 int qmag_trace_read(void *dst, size_t bytes)
@@ -337,7 +359,7 @@ int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, i
     if (st) return st;
     if (n_in <= 0 || n_in % QK_K || T <= 0) return fail(QMAG_ERR_ARG, "matmul: n_in=%d T=%d", n_in, T);
     // one token: the matvec quantises x itself (one launch)
-    if (T == 1) return launch_matvec_x(x, W, n_in, n_out, wtype, out, g_ctx.stream);
+    if (T == 1 && matvec_x_supported(n_in)) return launch_matvec_x(x, W, n_in, n_out, wtype, out, g_ctx.stream);
     int8_t *xq = (int8_t *)workspace(WS_XQ, (size_t)T * n_in, &st);
     if (st) return st;
     float *xd = (float *)workspace(WS_XD, sizeof(float) * (size_t)T * (n_in / QK_K), &st);
@@ -391,14 +413,14 @@ static uint8_t *stage(size_t bytes)
 
 static void ensure_ready_or_abort(const char *fn)
 {
-    if (!g_ctx.ready && qmag_init(0) != QMAG_OK) compat_abort(fn);
+    if (!g_ctx.ready.load(std::memory_order_acquire) && qmag_init(0) != QMAG_OK) compat_abort(fn);
 }
 
 static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 int qma_q8k_available(void)
 {
-    if (g_ctx.ready) return 1;
+    if (g_ctx.ready.load(std::memory_order_acquire)) return 1;
     return qmag_init(0) == QMAG_OK ? 1 : 0;
 }
 
@@ -455,6 +477,7 @@ float qma_q8k_dot(const void *row, int wtype, const int8_t *xq, const float *xd,
                   const int16_t *xsum, int n)
 {
     if (wtype != QMAG_TYPE_Q4_K && wtype != QMAG_TYPE_Q6_K) return 0.0f;   // q8k.c:314-315
+    n -= n % QK_K;                     // whole super-blocks only, as q8k.c:92 (nb = n / QK_K)
     if (n <= 0) return 0.0f;
     float out = 0.0f;
     compat_dot(&row, 1, wtype, xq, xd, xsum, n, &out, "qma_q8k_dot");
@@ -464,6 +487,7 @@ float qma_q8k_dot(const void *row, int wtype, const int8_t *xq, const float *xd,
 void qma_q8k_gateup(const void *g, const void *u, const int8_t *xq, const float *xd,
                     const int16_t *xsum, int n, float *gate, float *up)
 {
+    n -= n % QK_K;                     // whole super-blocks only (q8k.c:143)
     if (n <= 0) {
         *gate = *up = 0.0f;
         return;
@@ -473,6 +497,81 @@ void qma_q8k_gateup(const void *g, const void *u, const int8_t *xq, const float 
     compat_dot(rows, 2, QMAG_TYPE_Q4_K, xq, xd, xsum, n, out, "qma_q8k_gateup");
     *gate = out[0];
     *up = out[1];
+}
+
+/* ---------------------------------------------------------------------- */
+/* The fp32 entries of src/quants.c (qma.h:348-351): dequantisation and the */
+/* dequantise-then-dot row products, on the GPU through the calling        */
+/* thread's staging buffer like the q8k entries above.                     */
+/* ---------------------------------------------------------------------- */
+
+static void compat_dequant(const void *blocks, int wtype, int64_t k, float *y, const char *fn)
+{
+    ensure_ready_or_abort(fn);
+    const int64_t nb = k / QK_K;       // whole super-blocks, as quants.c:30 / :51
+    if (nb <= 0) return;
+    const size_t wb = (size_t)nb * (wtype == QMAG_TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES);
+    const size_t oy = a256(wb), tot = oy + sizeof(float) * (size_t)nb * QK_K;
+    uint8_t *b = stage(tot);
+    if (!b) compat_abort(fn);
+    hipStream_t s = t_stage.s;
+    bool ok = hipMemcpyAsync(b, blocks, wb, hipMemcpyHostToDevice, s) == hipSuccess;
+    ok = ok && launch_dequant(b, wtype, (long)(nb * QK_K), (float *)(b + oy), s) == QMAG_OK;
+    ok = ok && hipMemcpyAsync(y, b + oy, sizeof(float) * (size_t)nb * QK_K, hipMemcpyDeviceToHost, s) == hipSuccess;
+    ok = ok && hipStreamSynchronize(s) == hipSuccess;
+    if (!ok) compat_abort(fn);
+}
+
+static float compat_dot_f32(const void *row, int wtype, const float *x, int n, const char *fn)
+{
+    ensure_ready_or_abort(fn);
+    n -= n % QK_K;                     // whole super-blocks, as quants.c:81 / :109
+    if (n <= 0) return 0.0f;
+    const size_t bb = wtype == QMAG_TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    const size_t wb = (size_t)(n / QK_K) * bb;
+    // rows longer than the kernel's LDS-resident x run as chunks of at most
+    // F32_DOT_CHUNK values, summed here in chunk order
+    constexpr int F32_DOT_CHUNK = 8192;
+    const int nch = (n + F32_DOT_CHUNK - 1) / F32_DOT_CHUNK;
+    const size_t ox = a256(wb), oo = ox + a256(sizeof(float) * (size_t)n), tot = oo + a256(sizeof(float) * nch);
+    uint8_t *b = stage(tot);
+    if (!b) compat_abort(fn);
+    hipStream_t s = t_stage.s;
+    float part[(1 << 20) / F32_DOT_CHUNK];
+    if (nch > (int)(sizeof(part) / sizeof(part[0]))) compat_abort(fn);
+    bool ok = hipMemcpyAsync(b, row, wb, hipMemcpyHostToDevice, s) == hipSuccess;
+    ok = ok && hipMemcpyAsync(b + ox, x, sizeof(float) * (size_t)n, hipMemcpyHostToDevice, s) == hipSuccess;
+    for (int c = 0; c < nch && ok; c++) {
+        const int c0 = c * F32_DOT_CHUNK, cn = n - c0 < F32_DOT_CHUNK ? n - c0 : F32_DOT_CHUNK;
+        ok = launch_f32dot((const float *)(b + ox) + c0, b + (size_t)(c0 / QK_K) * bb, cn, 1, 1, wtype,
+                           (float *)(b + oo) + c, s) == QMAG_OK;
+    }
+    ok = ok && hipMemcpyAsync(part, b + oo, sizeof(float) * nch, hipMemcpyDeviceToHost, s) == hipSuccess;
+    ok = ok && hipStreamSynchronize(s) == hipSuccess;
+    if (!ok) compat_abort(fn);
+    float out = 0.0f;
+    for (int c = 0; c < nch; c++) out += part[c];
+    return out;
+}
+
+void dequantize_row_q4_K(const void *x, float *y, int64_t k)
+{
+    compat_dequant(x, QMAG_TYPE_Q4_K, k, y, "dequantize_row_q4_K");
+}
+
+void dequantize_row_q6_K(const void *x, float *y, int64_t k)
+{
+    compat_dequant(x, QMAG_TYPE_Q6_K, k, y, "dequantize_row_q6_K");
+}
+
+float dot_q4_K_f32(const void *W, const float *x, int n)
+{
+    return compat_dot_f32(W, QMAG_TYPE_Q4_K, x, n, "dot_q4_K_f32");
+}
+
+float dot_q6_K_f32(const void *W, const float *x, int n)
+{
+    return compat_dot_f32(W, QMAG_TYPE_Q6_K, x, n, "dot_q6_K_f32");
 }
 
 }  // extern "C"

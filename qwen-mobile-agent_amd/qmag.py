@@ -28,6 +28,10 @@ SIGNATURES = {
     "qma_q8k_quant": (None, [P, C.c_int, P, P, P]),
     "qma_q8k_dot": (C.c_float, [P, C.c_int, P, P, P, C.c_int]),
     "qma_q8k_gateup": (None, [P, P, P, P, P, C.c_int, P, P]),
+    "dequantize_row_q4_K": (None, [P, P, C.c_int64]),
+    "dequantize_row_q6_K": (None, [P, P, C.c_int64]),
+    "dot_q4_K_f32": (C.c_float, [P, P, C.c_int]),
+    "dot_q6_K_f32": (C.c_float, [P, P, C.c_int]),
     "qmag_init": (C.c_int, [C.c_int]),
     "qmag_last_error": (C.c_char_p, []),
     "qmag_device_info": (C.c_int, [P, P, P, C.c_char_p, C.c_int]),
@@ -43,10 +47,13 @@ SIGNATURES = {
     "qmag_prof_enable": (C.c_int, [C.c_int]),
     "qmag_prof_read": (C.c_int, [C.c_int, C.POINTER(C.c_long), C.POINTER(C.c_double)]),
     "qmag_set_option": (C.c_int, [C.c_int, C.c_int]),
+    "qmag_fused_recoveries": (C.c_int, [C.POINTER(C.c_long)]),
     "qmag_trace_read": (C.c_int, [P, C.c_size_t]),
     "qmag_q8k_quant_dev": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
     "qmag_matmul_q8k_dev": (C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_matmul_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+    "qmag_dequant_dev": (C.c_int, [P, C.c_int, C.c_int64, P]),
+    "qmag_matmul_f32_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_moe_ffn_dev": (C.c_int, [P, P, P, C.c_int]),
     "qmag_moe_stack_dev": (C.c_int, [P, C.c_int, P, C.c_int]),
     "qmag_moe_last_stage": (C.c_int, [C.POINTER(P)] * 5),
@@ -130,6 +137,21 @@ def set_grouped(on: bool) -> None:
     """Batches of >= 8 tokens: the grouped int8-MFMA expert GEMM (default) or
     the per-token launch sequence."""
     check(lib().qmag_set_option(OPT_GROUPED, 1 if on else 0))
+
+
+OPT_TEST_ABORT = 5
+
+
+def arm_test_abort(nth: int = 1) -> None:
+    """Make the nth persistent decode launch from now find its abort word set
+    (tests of the recovery path)."""
+    check(lib().qmag_set_option(OPT_TEST_ABORT, nth))
+
+
+def fused_recoveries() -> int:
+    n = C.c_long()
+    check(lib().qmag_fused_recoveries(C.byref(n)))
+    return n.value
 
 
 def trace_read(n_layer: int) -> np.ndarray:
@@ -216,6 +238,14 @@ def matmul_q8k_dev(xq, xd, xs, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> Non
 
 def matmul_dev(x: DBuf, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> None:
     check(lib().qmag_matmul_dev(x.ptr, W.ptr, n_in, n_out, T, wtype, out.ptr))
+
+
+def dequant_dev(W: DBuf, wtype: int, n: int, y: DBuf) -> None:
+    check(lib().qmag_dequant_dev(W.ptr, wtype, n, y.ptr))
+
+
+def matmul_f32_dev(x: DBuf, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> None:
+    check(lib().qmag_matmul_f32_dev(x.ptr, W.ptr, n_in, n_out, T, wtype, out.ptr))
 
 
 def moe_ffn_dev(layer: MoeLayer, x_ptr: int, out_ptr: int, T: int) -> None:

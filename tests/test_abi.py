@@ -13,7 +13,7 @@ HEADER = os.path.join(ROOT, "include", "qma_gpu.h")
 def declared_functions():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    names = re.findall(r"\b(qmag?_[a-z0-9_]+)\s*\(", src)
+    names = re.findall(r"\b((?:qmag?_|dequantize_row_|dot_q)[A-Za-z0-9_]+)\s*\(", src)
     return sorted(set(names))
 
 
@@ -28,7 +28,8 @@ def built():
 
 def test_header_declares_reference_entries():
     names = declared_functions()
-    for ref in ("qma_q8k_available", "qma_q8k_quant", "qma_q8k_dot", "qma_q8k_gateup"):
+    for ref in ("qma_q8k_available", "qma_q8k_quant", "qma_q8k_dot", "qma_q8k_gateup",
+                "dequantize_row_q4_K", "dequantize_row_q6_K", "dot_q4_K_f32", "dot_q6_K_f32"):
         assert ref in names
 
 

@@ -1,0 +1,229 @@
+"""GPU parity of the rest of the boundary, through the C-ABI, against the CPU
+oracle on the same bytes:
+
+* dequantisation (quants.c:29-75) bit-exact, also for fp16 block scales that
+  are subnormal, infinite or NaN (the GPU decodes fp16 in hardware);
+* the fp32 dequantise-then-dot matvec and the quants.c row entries
+  (quants.c:80-133) within 1e-4 of max|y|;
+* the q8k entries at row lengths that are not powers of two (q8k.c:92 takes
+  any whole number of super-blocks), and called from 8 host threads at once
+  as the engine's pool does (nn.c:276-289, 652-706);
+* the matmul seam at the engine's other projection shapes (qma.h:196-199:
+  wq 2048 -> 8192, wk / wv 2048 -> 512, wo 4096 -> 2048; wv's type varies).
+"""
+import ctypes as C
+import threading
+
+import numpy as np
+import pytest
+
+from conftest import max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _rand_blocks(rng, wtype, nb, special=False):
+    """Random-byte blocks (every bit pattern is a legal block) with fp16
+    scales drawn from normal magnitudes or, with special, from the edge
+    cases: subnormals, zero, +-Inf, NaN."""
+    size = 144 if wtype == 12 else 210
+    raw = rng.integers(0, 256, size=(nb, size), dtype=np.uint8)
+    if special:
+        pool = np.array([0x0001, 0x03FF, 0x8200, 0x0000, 0x8000, 0x7C00, 0xFC00, 0x7E00, 0x3C00, 0x0400],
+                        np.uint16)
+        d = pool[rng.integers(0, pool.size, nb)]
+        dm = pool[rng.integers(0, pool.size, nb)]
+    else:
+        d = rng.uniform(1e-4, 1e-2, nb).astype(np.float16).view(np.uint16)
+        dm = rng.uniform(1e-4, 1e-2, nb).astype(np.float16).view(np.uint16)
+    if wtype == 12:
+        raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        raw[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
+    else:
+        raw[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return raw.reshape(-1)
+
+
+def _same_bits_or_both_nan(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | (a.view(np.uint32) == b.view(np.uint32))))
+
+
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("special", [False, True])
+def test_dequant_dev_bit_exact(qm, orc, wtype, special):
+    rng = np.random.default_rng(wtype * 7 + special)
+    nb = 600
+    raw = _rand_blocks(rng, wtype, nb, special)
+    y = qm.DBuf(4 * 256 * nb)
+    qm.dequant_dev(qm.DBuf.from_array(raw), wtype, 256 * nb, y)
+    got = y.download(np.float32)
+    ref = orc.dequant(raw, wtype, 256 * nb)
+    assert _same_bits_or_both_nan(got, ref)
+
+
+@pytest.mark.parametrize("wtype", [12, 14])
+def test_dequant_row_entries(qm, orc, wtype):
+    """dequantize_row_q4_K / dequantize_row_q6_K with host pointers."""
+    L = qm.lib()
+    rng = np.random.default_rng(40 + wtype)
+    raw = _rand_blocks(rng, wtype, 8)
+    fn = L.dequantize_row_q4_K if wtype == 12 else L.dequantize_row_q6_K
+    y = np.full(2048 + 16, 7.0, np.float32)
+    fn(_p(raw), _p(y), 2048 + 100)          # only whole super-blocks (k / 256)
+    assert _same_bits_or_both_nan(y[:2048], orc.dequant(raw, wtype, 2048))
+    assert np.all(y[2048:] == 7.0)
+
+
+def test_q8k_dot_subnormal_scales(qm, orc):
+    """The int8 path with fp16 subnormal d / dmin (finite results)."""
+    rng = np.random.default_rng(3)
+    n_in, n_out = 2048, 256
+    for wtype in (12, 14):
+        raw = _rand_blocks(rng, wtype, n_out * 8)
+        b = raw.reshape(n_out * 8, -1)
+        sub = rng.integers(1, 0x400, (2, n_out * 8)).astype(np.uint16)     # fp16 subnormals
+        if wtype == 12:
+            b[:, 0:2] = sub[0].view(np.uint8).reshape(-1, 2)
+            b[:, 2:4] = sub[1].view(np.uint8).reshape(-1, 2)
+        else:
+            b[:, 208:210] = sub[0].view(np.uint8).reshape(-1, 2)
+        x = orc.fill_normal(9, n_in, 0.0, 1.0)
+        out = qm.DBuf(4 * n_out)
+        qm.matmul_dev(qm.DBuf.from_array(x), qm.DBuf.from_array(raw), n_in, n_out, 1, wtype, out)
+        ref = orc.matmul_q8k(x, raw, n_in, n_out, 1, wtype)[0]
+        assert max_rel_err(out.download(np.float32), ref) < TOL
+
+
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("n_in,n_out,T", [(256, 100, 1), (2048, 512, 1), (512, 2048, 3), (8192, 64, 2),
+                                          (768, 77, 1)])
+def test_matmul_f32_dev(qm, orc, wtype, n_in, n_out, T):
+    """The QMA_NOQ8K dequantise-then-dot path against the oracle's
+    dot_q4_K_f32 / dot_q6_K_f32 per row (quants.c:80-133)."""
+    W = orc.quantize(orc.fill_normal(500 + n_in + n_out, n_in * n_out, 0.0, 0.02), wtype)
+    x = orc.fill_normal(600 + T, T * n_in, 0.0, 1.0)
+    out = qm.DBuf(4 * T * n_out)
+    qm.matmul_f32_dev(qm.DBuf.from_array(x), qm.DBuf.from_array(W), n_in, n_out, T, wtype, out)
+    got = out.download(np.float32).reshape(T, n_out)
+    rb = W.size // n_out
+    for t in range(T):
+        ref = np.array([orc.dot_f32(W[r * rb:(r + 1) * rb], wtype, x[t * n_in:(t + 1) * n_in], n_in)
+                        for r in range(n_out)], np.float32)
+        assert max_rel_err(got[t], ref) < TOL
+
+
+@pytest.mark.parametrize("wtype", [12, 14])
+def test_dot_f32_entries(qm, orc, wtype):
+    """dot_q4_K_f32 / dot_q6_K_f32 with host pointers, over 64 rows (the
+    1e-4 bar is relative to the largest of the 64 results), including a row
+    longer than one 8192-value chunk."""
+    L = qm.lib()
+    fn = L.dot_q4_K_f32 if wtype == 12 else L.dot_q6_K_f32
+    for n in (2048, 512, 12288):
+        W = orc.quantize(orc.fill_normal(70 + n, 64 * n, 0.0, 0.02), wtype)
+        x = orc.fill_normal(71, n, 0.0, 1.0)
+        rb = W.size // 64
+        got = np.array([fn(_p(W[r * rb:]), _p(x), n) for r in range(64)], np.float32)
+        ref = np.array([orc.dot_f32(W[r * rb:(r + 1) * rb], wtype, x, n) for r in range(64)], np.float32)
+        assert max_rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("n_in", [768, 1280, 3072])
+def test_matmul_non_power_of_two_rows(qm, orc, wtype, n_in):
+    n_out, T = 300, 2
+    W = orc.quantize(orc.fill_normal(900 + n_in, n_in * n_out, 0.0, 0.02), wtype)
+    x = orc.fill_normal(901, T * n_in, 0.0, 1.0)
+    out = qm.DBuf(4 * T * n_out)
+    Wb = qm.DBuf.from_array(W)
+    for T_ in (1, T):
+        qm.matmul_dev(qm.DBuf.from_array(x[:T_ * n_in]), Wb, n_in, n_out, T_, wtype, out)
+        got = out.download(np.float32, T_ * n_out).reshape(T_, n_out)
+        ref = orc.matmul_q8k(x[:T_ * n_in], W, n_in, n_out, T_, wtype)
+        for t in range(T_):
+            assert max_rel_err(got[t], ref[t]) < TOL
+
+
+def test_compat_dot_any_length(qm, orc):
+    """qma_q8k_dot / qma_q8k_gateup at n = 768 and 1280 (not powers of two)."""
+    L = qm.lib()
+    for n in (768, 1280):
+        xq, xd, xs = orc.q8k_quant(orc.fill_normal(n, n, 0.0, 1.0))
+        rows = orc.quantize(orc.fill_normal(n + 1, 16 * n, 0.0, 0.02), 12).reshape(16, -1)
+        got = np.array([L.qma_q8k_dot(_p(r), 12, _p(xq), _p(xd), _p(xs), n) for r in rows], np.float32)
+        ref = np.array([orc.q8k_dot(r, 12, xq, xd, xs, n) for r in rows], np.float32)
+        assert max_rel_err(got, ref) < TOL
+        go, uo = C.c_float(), C.c_float()
+        L.qma_q8k_gateup(_p(rows[0]), _p(rows[1]), _p(xq), _p(xd), _p(xs), n, C.byref(go), C.byref(uo))
+        assert abs(go.value - ref[0]) <= TOL * np.abs(ref).max()
+        assert abs(uo.value - ref[1]) <= TOL * np.abs(ref).max()
+
+
+def test_compat_entries_concurrent_threads(qm, orc):
+    """Eight host threads call qma_q8k_dot, qma_q8k_gateup and dot_q4_K_f32
+    at once, as the pool workers do; every result matches the oracle."""
+    L = qm.lib()
+    n, rows_per = 2048, 24
+    xq, xd, xs = orc.q8k_quant(orc.fill_normal(5, n, 0.0, 1.0))
+    xf = orc.fill_normal(6, n, 0.0, 1.0)
+    W = orc.quantize(orc.fill_normal(7, 8 * 2 * rows_per * n, 0.0, 0.02), 12).reshape(8, 2 * rows_per, -1)
+    ref_q = np.array([[orc.q8k_dot(r, 12, xq, xd, xs, n) for r in W[k]] for k in range(8)], np.float32)
+    ref_f = np.array([[orc.dot_f32(r, 12, xf, n) for r in W[k]] for k in range(8)], np.float32)
+    got_q = np.zeros_like(ref_q)
+    got_g = np.zeros_like(ref_q)
+    got_f = np.zeros_like(ref_f)
+    errors = []
+    start = threading.Barrier(8)
+
+    def work(k):
+        try:
+            start.wait()
+            for i in range(2 * rows_per):
+                got_q[k, i] = L.qma_q8k_dot(_p(W[k, i]), 12, _p(xq), _p(xd), _p(xs), n)
+                got_f[k, i] = L.dot_q4_K_f32(_p(W[k, i]), _p(xf), n)
+            for i in range(0, 2 * rows_per, 2):
+                go, uo = C.c_float(), C.c_float()
+                L.qma_q8k_gateup(_p(W[k, i]), _p(W[k, i + 1]), _p(xq), _p(xd), _p(xs), n,
+                                 C.byref(go), C.byref(uo))
+                got_g[k, i], got_g[k, i + 1] = go.value, uo.value
+        except Exception as e:      # surfaced below
+            errors.append(e)
+
+    ts = [threading.Thread(target=work, args=(k,)) for k in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    assert not errors
+    assert max_rel_err(got_q, ref_q) < TOL
+    assert max_rel_err(got_g, ref_q) < TOL
+    assert max_rel_err(got_f, ref_f) < TOL
+
+
+@pytest.mark.parametrize("name,n_in,n_out,wtype", [
+    ("wq", 2048, 8192, 12), ("wk", 2048, 512, 12), ("wv_q4k", 2048, 512, 12), ("wv_q6k", 2048, 512, 14),
+    ("wo", 4096, 2048, 12), ("wo_q6k", 4096, 2048, 14)])
+def test_matmul_projection_shapes(qm, orc, name, n_in, n_out, wtype):
+    """The other matmul() call sites of qma_eval (nn.c:2111-2113, 2162,
+    2165-2170, 2243) at the engine's shapes (qma.h:196-199), T = 1 (decode)
+    and T = 5 (a prefill chunk)."""
+    W = orc.quantize(orc.fill_normal(sum(map(ord, name)) + n_in, n_in * n_out, 0.0, 0.02), wtype)
+    Wb = qm.DBuf.from_array(W)
+    orc.set_threads(8)
+    for T in (1, 5):
+        x = orc.fill_normal(T + n_in, T * n_in, 0.0, 1.0)
+        out = qm.DBuf(4 * T * n_out)
+        qm.matmul_dev(qm.DBuf.from_array(x), Wb, n_in, n_out, T, wtype, out)
+        got = out.download(np.float32).reshape(T, n_out)
+        ref = orc.matmul_q8k(x, W, n_in, n_out, T, wtype)
+        for t in range(T):
+            assert max_rel_err(got[t], ref[t]) < TOL, (name, T, t)
+    orc.set_threads(1)
