@@ -177,6 +177,20 @@ int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum,
 int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
                     float *out);
 
+/* The matmul seam without any allocation (no counterpart in the reference):
+   for callers that cannot allocate -- code under HIP graph capture, serving
+   loops that forbid hipMalloc.  Same arguments and results as
+   qmag_matmul_dev (the same kernels; bit-identical output), but the Q8_K
+   staging of the T activation rows lives in a fixed 2.4 MB array of device
+   memory each GPU holds for the life of the process, instead of a workspace
+   grown with hipMalloc.  Limit: T * n_in <= 2^21 (QMAG_ERR_ARG beyond).
+   Calls that overlap on one GPU share that array and race; issue them on the
+   library stream (every qmag entry does) and not from several threads at
+   once. */
+#define QMAG_NOALLOC_MAX_VALUES (1 << 21)
+int qmag_matmul_noalloc_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
+                            float *out);
+
 /* Dequantisation of n weights (n % 256 == 0) to f32, bit-identical to
    dequantize_row_q4_K / dequantize_row_q6_K (src/quants.c:29-75); the weight
    definition embed_row uses (nn.c:2044-2054). */

@@ -61,6 +61,13 @@ enum ProfId {
 bool prof_on();
 void prof_begin(int id, hipStream_t s);
 void prof_end(int id, hipStream_t s);
+// while one is alive on a thread, that thread's launches are not timed
+struct ProfSuspend {
+    ProfSuspend();
+    ~ProfSuspend();
+};
+// the allocation-free matmul's scratch address, looked up per device
+int noalloc_setup(int dev);
 
 // ---- launchers (all stream-ordered on s) ----
 int launch_q8k_quant(const float *x, int nblocks, int8_t *xq, float *xd, int16_t *xsum,

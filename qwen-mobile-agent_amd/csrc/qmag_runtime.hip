@@ -94,6 +94,10 @@ static hipEvent_t g_prof_open[PROF_COUNT];
 
 bool prof_on() { return g_prof; }
 
+static thread_local int t_prof_suspended = 0;
+ProfSuspend::ProfSuspend() { t_prof_suspended++; }
+ProfSuspend::~ProfSuspend() { t_prof_suspended--; }
+
 static hipEvent_t prof_event()
 {
     hipEvent_t e = nullptr;
@@ -111,14 +115,14 @@ static hipEvent_t prof_event()
 // never bracketed (the records below are not shared-state safe).
 void prof_begin(int id, hipStream_t s)
 {
-    if (!g_prof || s != g_ctx.stream) return;
+    if (!g_prof || s != g_ctx.stream || t_prof_suspended) return;
     hipEvent_t e = prof_event();
     if (e && hipEventRecord(e, s) == hipSuccess) g_prof_open[id] = e;
 }
 
 void prof_end(int id, hipStream_t s)
 {
-    if (!g_prof || s != g_ctx.stream || !g_prof_open[id]) return;
+    if (!g_prof || s != g_ctx.stream || t_prof_suspended || !g_prof_open[id]) return;
     hipEvent_t e = prof_event();
     if (e && hipEventRecord(e, s) == hipSuccess) g_prof_recs.push_back({id, g_prof_open[id], e});
     g_prof_open[id] = nullptr;
@@ -191,6 +195,8 @@ int qmag_init(int device)
         return fail(QMAG_ERR_NODEV, "device %d is %s; this library is built for gfx950", device,
                     prop.gcnArchName);
     QMAG_HIP(hipSetDevice(device));
+    int st = noalloc_setup(device);
+    if (st) return st;
     QMAG_HIP(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking));
     for (int i = 0; i < 64; i++) QMAG_HIP(hipEventCreate(&g_ctx.ev[i]));
     g_ctx.dev = device;

@@ -52,6 +52,7 @@ SIGNATURES = {
     "qmag_q8k_quant_dev": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
     "qmag_matmul_q8k_dev": (C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_matmul_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+    "qmag_matmul_noalloc_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_dequant_dev": (C.c_int, [P, C.c_int, C.c_int64, P]),
     "qmag_matmul_f32_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_moe_ffn_dev": (C.c_int, [P, P, P, C.c_int]),
