@@ -416,4 +416,31 @@ __device__ __forceinline__ int q6_int_dot(const Q6Raw &r, const Q6Act &a, int l1
     return tot;
 }
 
+// ---------------------------------------------------------- routing ----
+// The reference's softmax (nn.c:517-527) turns every probability into NaN
+// when one logit is NaN or +Inf (its term is NaN), or when every logit is at
+// or below its -1e30 starting maximum (the sum is 0).  Then no `p > -1e30`
+// test of the top-K scan holds and every pick is expert 0 with value -1e30
+// (nn.c:529-533), renormalised to -1e30 / (K * -1e30) summed in pick order.
+// The E <= 256 logits sit 4 per lane of one wave, expert lane + 64j.
+__device__ __forceinline__ bool route_degenerate(const float (&l)[4], int E)
+{
+    bool bad = false;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (lane_id() + 64 * j < E) {
+            bad = bad || !(l[j] < INFINITY);            // NaN or +Inf
+            mx = fmaxf(mx, l[j]);
+        }
+    }
+    return __ballot(bad) != 0 || group_max<64>(mx) <= -1e30f;
+}
+__device__ __forceinline__ float route_degenerate_weight(int K)
+{
+    float ws = 0.0f;
+    for (int k = 0; k < K; k++) ws += -1e30f;
+    return -1e30f / ws;
+}
+
 }  // namespace qmag

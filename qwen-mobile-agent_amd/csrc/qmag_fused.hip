@@ -340,6 +340,9 @@ __device__ __forceinline__ float d_dot(const DRaw<TD> &d, const uint32_t *hq, co
 // operands (three instructions per step instead of one).
 __device__ __forceinline__ int f2key(float v)
 {
+    // (route_topk handles NaN logits before it makes keys; this keeps the
+    // order total all the same)
+    if (v != v) return INT_MIN;
     const int b = __float_as_int(v + 0.0f);
     return b >= 0 ? b : b ^ 0x7fffffff;
 }
@@ -350,11 +353,50 @@ __device__ __forceinline__ float key2f(int k) { return __int_as_float(k >= 0 ? k
 // value left, the lowest index among equal values (the reference's strict-`>`
 // scan from e = 0).  The selection is made on the logits (softmax is
 // monotonic) through their integer keys; each lane sorts its four candidates
-// once, and a pick is one wave max over the lane heads, one ballot for the
-// winning lane and a shift of that lane's list.  Lane k < K receives pick k:
-// its expert id and its weight exp(l_k - l_max) / sum over the K picks, the
-// reference's p_k / sum_sel p with the full softmax sum cancelled (summed in
-// pick order).
+// once, and a pick is one wave max over the lane heads and a shift of the
+// winning lane's list.  Lane k < K receives pick k: its expert id and its
+// weight exp(l_k - l_max) / sum over the K picks, the reference's
+// p_k / sum_sel p with the full softmax sum cancelled (summed in pick order).
+//
+// The picks run a fast path first: the winning lane is the one whose head
+// equals the maximum, a vector compare, so no pick waits for a scalar round
+// trip.  That is exact unless two heads are equal; every pick's ballot is
+// checked off the critical path, and if any pick saw such a tie the picks are
+// made again with the tie rule (lowest index among the equal heads).
+template <bool EXACT>
+__device__ __forceinline__ bool topk_picks(const int (&v0)[4], const int (&id0)[4], int K, int lane, int &sel,
+                                           int &my_key)
+{
+    int v[4] = {v0[0], v0[1], v0[2], v0[3]}, id[4] = {id0[0], id0[1], id0[2], id0[3]};
+    unsigned long long tie = 0;
+    for (int k = 0; k < K; k++) {
+        const int m = group_max_i<64>(v[0]);
+        bool me = v[0] == m;
+        unsigned long long bal = __ballot(me);
+        if constexpr (EXACT) {
+            if (bal & (bal - 1)) {              // exact tie: the lowest index wins (one wave min)
+                const int best = group_min_i<64>(me ? id[0] : INT_MAX);
+                me = me && id[0] == best;
+                bal = __ballot(me);
+            }
+        } else {
+            tie |= bal & (bal - 1);
+        }
+        const int id_head = id[0];
+        v[0] = me ? v[1] : v[0];
+        v[1] = me ? v[2] : v[1];
+        v[2] = me ? v[3] : v[2];
+        v[3] = me ? INT_MIN : v[3];
+        id[0] = me ? id[1] : id[0];
+        id[1] = me ? id[2] : id[1];
+        id[2] = me ? id[3] : id[2];
+        const int e = __builtin_amdgcn_readlane(id_head, __builtin_ctzll(bal));
+        sel = lane == k ? e : sel;
+        my_key = lane == k ? m : my_key;
+    }
+    return tie == 0;
+}
+
 __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, float &my_w)
 {
     const int lane = lane_id();
@@ -377,40 +419,25 @@ __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, floa
     cswap(0, 2);
     cswap(1, 3);
     cswap(1, 2);
+    bool nan_here = false;
+#pragma unroll
+    for (int j = 0; j < 4; j++) nan_here = nan_here || (lane + 64 * j < E && lg[j] != lg[j]);
+    const bool any_nan = __ballot(nan_here) != 0;
     int my_key = INT_MIN, sel = 0;
-    for (int k = 0; k < K; k++) {
-        const int m = group_max_i<64>(v[0]);
-        unsigned long long bal = __ballot(v[0] == m);
-        int win = __builtin_ctzll(bal);         // some lane holds the maximum
-        if (bal & (bal - 1)) {                  // exact tie: the lowest index wins
-            int best = __builtin_amdgcn_readlane(id[0], win);
-            for (bal &= bal - 1; bal; bal &= bal - 1) {
-                const int ln = __builtin_ctzll(bal);
-                const int c = __builtin_amdgcn_readlane(id[0], ln);
-                if (c < best) {
-                    best = c;
-                    win = ln;
-                }
-            }
-        }
-        const int e = __builtin_amdgcn_readlane(id[0], win);
-        const bool me = lane == win;
-        v[0] = me ? v[1] : v[0];
-        v[1] = me ? v[2] : v[1];
-        v[2] = me ? v[3] : v[2];
-        v[3] = me ? INT_MIN : v[3];
-        id[0] = me ? id[1] : id[0];
-        id[1] = me ? id[2] : id[1];
-        id[2] = me ? id[3] : id[2];
-        sel = lane == k ? e : sel;
-        my_key = lane == k ? m : my_key;
-    }
+    if (!topk_picks<false>(v, id, K, lane, sel, my_key)) topk_picks<true>(v, id, K, lane, sel, my_key);
     const float l0 = key2f(__builtin_amdgcn_readfirstlane(my_key));
+    // the reference's softmax is NaN throughout when a logit is NaN or +Inf,
+    // or when every logit is at or below -1e30 (see route_degenerate): then
+    // it picks expert 0 K times
+    if (any_nan || !(l0 < INFINITY) || l0 <= -1e30f) {
+        if (lane < K) my_sel = 0;
+        my_w = route_degenerate_weight(K);
+        return;
+    }
     if (lane < K) my_sel = sel;
     const float ex = lane < K ? expf(key2f(my_key) - l0) : 0.0f;
     my_w = ex / group_sum<8>(ex);
 }
-
 
 template <int TD>
 __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer *__restrict__ layers,

@@ -12,6 +12,8 @@
 //   down_kernel     out[r] = sum_k w_k * down_k[r] . Q8_K(h_k) + gs * down_sh[r] . Q8_K(h_sh)
 //                   in the reference's combine order (k = 0..n_used-1, then shared),
 //                   optionally plus a residual                         nn.c:435-437, 468-472, 614-629
+#include <limits.h>
+
 #include "qmag_internal.h"
 
 namespace qmag {
@@ -118,7 +120,12 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
     g = group_sum<64>(g);
     if (lane == 0) s_red[wv] = g;
 
-    if (wv == 0) {
+    if (wv == 0 && route_degenerate(l, E)) {      // the reference's NaN softmax: expert 0, K times
+        if (lane < K) {
+            sel[(size_t)t * K + lane] = 0;
+            wout[(size_t)t * K + lane] = route_degenerate_weight(K);
+        }
+    } else if (wv == 0) {
         // softmax over E <= 256 logits, 4 per lane
         float mx = -INFINITY;
 #pragma unroll
@@ -152,19 +159,12 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
         int sk = 0;
         for (int k = 0; k < K; k++) {
             const float m = group_max<64>(p[0]);
-            unsigned long long bal = __ballot(p[0] == m);
+            const unsigned long long bal = __ballot(p[0] == m);
             // a NaN maximum equals nothing: fall back to lane 0's head, in range
             int win = bal ? __builtin_ctzll(bal) : 0;
-            if (bal & (bal - 1)) {                // exact tie: the lowest index wins
-                int best = __builtin_amdgcn_readlane(id[0], win);
-                for (bal &= bal - 1; bal; bal &= bal - 1) {
-                    const int ln = __builtin_ctzll(bal);
-                    const int e = __builtin_amdgcn_readlane(id[0], ln);
-                    if (e < best) {
-                        best = e;
-                        win = ln;
-                    }
-                }
+            if (bal & (bal - 1)) {                // exact tie: the lowest index wins (one wave min)
+                const int best = group_min_i<64>(p[0] == m ? id[0] : INT_MAX);
+                win = __builtin_ctzll(__ballot(p[0] == m && id[0] == best));
             }
             const int e = __builtin_amdgcn_readlane(id[0], win);
             if (lane == k) {

@@ -563,3 +563,53 @@ def test_stack_small_n_used(qm, orc, n_used):
         qm.set_fused(True)
     for r in rls:
         r.close()
+
+
+@pytest.mark.parametrize("case", ["nan_row", "inf_bias", "all_below_1e30"])
+@pytest.mark.parametrize("path", ["fused", "sequence", "grouped"])
+def test_route_degenerate_softmax(qm, orc, case, path):
+    """When the reference's softmax is NaN throughout -- a NaN logit, a +Inf
+    logit, or every logit at or below its -1e30 starting maximum -- its top-K
+    scan picks expert 0 for every slot with weight -1e30 / (K * -1e30)
+    (nn.c:517-536).  Every GPU path makes the same picks and weights, and the
+    output (expert 0 eight times plus the shared expert) matches the oracle
+    stage by stage."""
+    E, K, N, F = 32, 8, 2048, 512
+    hl = make_host_layer(orc, seed=88, n_embd=N, n_ff=F, n_expert=E, n_used=K, router_bias_std=0.0)
+    wr = hl.gate_inp.reshape(E, N)
+    bias = hl.router_bias
+    if case == "nan_row":
+        wr[5, 100] = np.nan
+    elif case == "inf_bias":
+        bias[9] = np.inf
+    else:
+        bias[:] = -2e30
+    rl = qm.ResidentLayer.from_host(hl)
+    T = 16 if path == "grouped" else 1
+    x = orc.fill_normal(19, T * N, 0.0, 1.0)
+    qm.set_fused(path == "fused")
+    try:
+        got = run_layer(qm, rl, x, T)
+        st = qm.moe_last_stage(E, K, F, n_tok=T)
+    finally:
+        qm.set_fused(True)
+    gb, db = hl.gate_exps.size // E, hl.down_exps.size // E
+    for t in range(T):
+        xt = x[t * N:(t + 1) * N]
+        sel_o, w_o, _ = orc.moe_route(hl, xt)
+        assert list(sel_o) == [0] * K
+        assert list(st["sel"][t]) == list(sel_o), f"token {t}"
+        assert np.array_equal(st["w"][t].view(np.uint32), w_o.view(np.uint32)), f"token {t}"
+        xq, xd, xs = orc.q8k_quant(xt)
+        h0 = orc.moe_expert_h(hl.gate_exps[:gb], hl.up_exps[:gb], N, F, xq, xd, xs)
+        acc = np.zeros(N, np.float32)
+        for s in range(K + 1):
+            if s < K:
+                assert max_rel_err(st["h"][t][s], h0) < TOL
+                dn, scale = hl.down_exps[:db], st["w"][t][s]
+            else:
+                dn, scale = hl.down_shexp, st["gs"][t]
+            y = orc.matmul_q8k(st["h"][t][s], dn, F, N, 1, hl.t_down_exps)[0]
+            acc = (acc + (np.float32(scale) * y).astype(np.float32)).astype(np.float32)
+        assert max_rel_err(got[t], acc) < TOL, f"output, token {t}"
+    rl.close()
