@@ -243,6 +243,45 @@ int qmag_moe_last_stage(const float **logits, const int **sel, const float **w,
                         const float **gs, const float **h);
 
 /* ------------------------------------------------------------------------ */
+/* GGUF v3 weights into HBM residency (the loader role of src/gguf.c)        */
+/* ------------------------------------------------------------------------ */
+
+/* An opened, indexed GGUF file: mapped read-only; tensor data is not read
+   until a tensor is uploaded. */
+typedef struct qmag_gguf qmag_gguf;
+
+/* Open and index a GGUF (v2/v3) file: header, integer metadata (keys with the
+   qwen35moe./qwen35. architecture prefix stripped, gguf.c:146-153), the tensor
+   table and the aligned data section (general.alignment, default 32).  As
+   qma_load (gguf.c:104-283) it fails (QMAG_ERR_ARG, message in
+   qmag_last_error) on a bad magic, truncated or corrupt tables, a tensor
+   outside the file, a first dimension that is not a whole number of blocks,
+   or a tensor type other than F32 (0), Q4_K (12) and Q6_K (14).  Needs no
+   GPU. */
+int qmag_gguf_open(const char *path, qmag_gguf **out);
+void qmag_gguf_close(qmag_gguf *g);
+/* An integer metadata value ("block_count", "expert_count", ...; the
+   architecture prefix is optional). */
+int qmag_gguf_meta_u64(const qmag_gguf *g, const char *key, uint64_t *val);
+/* A tensor's GGML type, dimensions (ne[0] fastest) and host bytes in the
+   mapping (valid until qmag_gguf_close). */
+int qmag_gguf_tensor(const qmag_gguf *g, const char *name, int *type, int64_t ne[3], const void **data,
+                     size_t *nbytes);
+/* Copy one tensor to a new device allocation (free with qmag_free), e.g.
+   output.weight for the LM-head matmul (nn.c:2286). */
+int qmag_gguf_upload_tensor(const qmag_gguf *g, const char *name, void **dptr, int *type, int64_t ne[3]);
+/* Upload layer il's MoE FFN tensors -- blk.<il>.ffn_{gate_inp, gate_exps,
+   up_exps, down_exps, gate_inp_shexp, gate_shexp, up_shexp, down_shexp}
+   (gguf.c:318-326) -- each as one contiguous copy (expert-major slabs,
+   gguf.c:268-271), and fill *L with the device pointers, the shapes from the
+   tensor dimensions, the per-layer down types, and n_used from
+   expert_used_count (8 if absent, qma.h:58).  Gate/up must be Q4_K and the
+   expert and shared hidden sizes equal. */
+int qmag_gguf_upload_moe_layer(const qmag_gguf *g, int il, qmag_moe_layer *L);
+/* Free the device tensors of a layer filled by qmag_gguf_upload_moe_layer. */
+int qmag_gguf_free_moe_layer(qmag_moe_layer *L);
+
+/* ------------------------------------------------------------------------ */
 /* Synthetic inputs (bench/test utilities; not part of the reference)        */
 /* ------------------------------------------------------------------------ */
 

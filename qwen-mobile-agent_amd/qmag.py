@@ -58,6 +58,14 @@ SIGNATURES = {
     "qmag_moe_ffn_dev": (C.c_int, [P, P, P, C.c_int]),
     "qmag_moe_stack_dev": (C.c_int, [P, C.c_int, P, C.c_int]),
     "qmag_moe_last_stage": (C.c_int, [C.POINTER(P)] * 5),
+    "qmag_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+    "qmag_gguf_close": (None, [P]),
+    "qmag_gguf_meta_u64": (C.c_int, [P, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "qmag_gguf_tensor": (C.c_int, [P, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int64), C.POINTER(P),
+                                   C.POINTER(C.c_size_t)]),
+    "qmag_gguf_upload_tensor": (C.c_int, [P, C.c_char_p, C.POINTER(P), C.POINTER(C.c_int), C.POINTER(C.c_int64)]),
+    "qmag_gguf_upload_moe_layer": (C.c_int, [P, C.c_int, P]),
+    "qmag_gguf_free_moe_layer": (C.c_int, [P]),
     "qmag_synth_normal": (C.c_int, [C.c_uint64, C.c_size_t, C.c_float, C.c_float, P]),
     "qmag_synth_weights": (C.c_int, [C.c_uint64, C.c_size_t, C.c_float, C.c_int, P]),
     "qmag_quantize_dev": (C.c_int, [P, C.c_size_t, C.c_int, P]),
@@ -401,3 +409,53 @@ class ResidentLayer:
             b = getattr(self, k, None)
             if b is not None:
                 b.close()
+
+
+# ------------------------------------------------------------------ GGUF --
+
+class Gguf:
+    """An opened GGUF file (qmag_gguf_open); tensor queries need no GPU,
+    uploads do."""
+
+    def __init__(self, path: str):
+        h = P()
+        check(lib().qmag_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h.value
+
+    def meta(self, key: str) -> int:
+        v = C.c_uint64()
+        check(lib().qmag_gguf_meta_u64(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def tensor(self, name: str):
+        """(type, (ne0, ne1, ne2), bytes as a numpy uint8 view copy)."""
+        t, ne, data, nb = C.c_int(), (C.c_int64 * 3)(), P(), C.c_size_t()
+        check(lib().qmag_gguf_tensor(self.h, name.encode(), C.byref(t), ne, C.byref(data), C.byref(nb)))
+        buf = (C.c_uint8 * nb.value).from_address(data.value)
+        return t.value, tuple(ne), np.frombuffer(buf, dtype=np.uint8).copy()
+
+    def upload_tensor(self, name: str):
+        """Device pointer (free with qmag_free), type, dims."""
+        d, t, ne = P(), C.c_int(), (C.c_int64 * 3)()
+        check(lib().qmag_gguf_upload_tensor(self.h, name.encode(), C.byref(d), C.byref(t), ne))
+        return d.value, t.value, tuple(ne)
+
+    def upload_moe_layer(self, il: int) -> MoeLayer:
+        L = MoeLayer()
+        check(lib().qmag_gguf_upload_moe_layer(self.h, il, C.byref(L)))
+        return L
+
+    @staticmethod
+    def free_moe_layer(L: MoeLayer) -> None:
+        check(lib().qmag_gguf_free_moe_layer(C.byref(L)))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().qmag_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
