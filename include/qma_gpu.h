@@ -42,7 +42,9 @@ extern "C" {
 #define QMAG_ERR_KERNEL (-4)   /* a kernel reported an internal guard trip   */
 /* Buffers passed to the device entries must stay valid until the next
    qmag_sync or qmag_d2h: the library may re-run the calls issued since the
-   previous one (see qmag_fused_recoveries). */
+   previous one (see qmag_fused_recoveries).  Only those MoE calls are re-run:
+   other device work queued after them that read their outputs (an LM-head
+   matmul, say) is re-queued by the caller when qmag_fused_recoveries rises. */
 
 /* ------------------------------------------------------------------------ */
 /* Reference-compatible entries                                              */
@@ -280,6 +282,42 @@ int qmag_gguf_upload_tensor(const qmag_gguf *g, const char *name, void **dptr, i
 int qmag_gguf_upload_moe_layer(const qmag_gguf *g, int il, qmag_moe_layer *L);
 /* Free the device tensors of a layer filled by qmag_gguf_upload_moe_layer. */
 int qmag_gguf_free_moe_layer(qmag_moe_layer *L);
+
+/* ------------------------------------------------------------------------ */
+/* Sampling on the device (src/sampler.c), logits resident in HBM            */
+/* ------------------------------------------------------------------------ */
+
+/* The sampler state, field for field the layout of sampler_t (qma.h:279-287),
+   so a sampler_t * may be passed where a qmag_sampler * is expected. */
+typedef struct qmag_sampler {
+    uint64_t seed;
+    float temp;
+    int top_k;
+    float top_p;
+    float repeat_penalty;
+    int last_tokens[64];
+    int n_last;
+} qmag_sampler;
+
+/* sampler_candidates (sampler.c:36-95, qma.h:338) on device logits: the
+   repeat penalty per occurrence in last_tokens, division by temp when
+   temp > 0, and the k = clamp(top_k, 1, min(n_vocab, max_k)) largest values
+   in descending order, ids and values copied to the host arrays ids[k],
+   lgs[k] (agent.c:935 asks for 40).  Returns k (>= 1) or a negative status.  max_k <= 64,
+   n_vocab <= 520192.  Equal values are ordered by ascending id (the
+   reference's order among exact ties follows its heap). */
+int qmag_sampler_candidates_dev(int n_vocab, const float *logits, const qmag_sampler *s, int *ids, float *lgs,
+                                int max_k);
+/* sampler_candidates followed by sampler_pick (sampler.c:100-134) on the
+   unmasked candidates, both on the device; only the token id comes back.
+   Matches the reference call pair with no grammar mask between them: the
+   greedy answer at temp <= 0; otherwise the softmax with a double sum, the
+   top-p cut, one xorshift64* draw (s->seed advances) and the pick joining
+   s->last_tokens (the last 64 kept).  Replaces the pair at agent.c:935-955
+   when no grammar mask runs (tool_mode off); with the mask, call
+   qmag_sampler_candidates_dev and the host's sampler_pick on its 40. */
+int qmag_sampler_sample_dev(int n_vocab, const float *logits, qmag_sampler *s, int max_k, float top_p,
+                            int *token);
 
 /* ------------------------------------------------------------------------ */
 /* Synthetic inputs (bench/test utilities; not part of the reference)        */

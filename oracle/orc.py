@@ -74,8 +74,42 @@ def _declare(L):
     L.orc_moe_shared_gate.argtypes = [P, P, P, C.c_int]
     L.orc_moe_stack.argtypes = [C.POINTER(MoeLayer), C.c_int, P]
     L.orc_fill_normal.argtypes = [C.c_uint64, C.c_int64, C.c_float, C.c_float, P]
+    L.orc_sampler_candidates.restype = C.c_int
+    L.orc_sampler_candidates.argtypes = [C.c_int, P, C.POINTER(Sampler), P, P, C.c_int]
+    L.orc_sampler_pick.restype = C.c_int
+    L.orc_sampler_pick.argtypes = [C.POINTER(Sampler), P, P, C.c_int, C.c_float]
     L.orc_quantize_q4k.argtypes = [P, C.c_int64, P]
     L.orc_quantize_q6k.argtypes = [P, C.c_int64, P]
+
+
+class Sampler(C.Structure):
+    """sampler_t (qma.h:279-287)."""
+    _fields_ = [("seed", C.c_uint64), ("temp", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("last_tokens", C.c_int * 64), ("n_last", C.c_int)]
+
+
+def make_sampler(seed=1, temp=0.7, top_k=20, top_p=0.95, repeat_penalty=1.0, last=()):
+    s = Sampler()
+    s.seed = seed if seed else 0x9E3779B97F4A7C15        # sampler_init, sampler.c:16-23
+    s.temp, s.top_k, s.top_p, s.repeat_penalty = temp, top_k, top_p, repeat_penalty
+    for i, t in enumerate(last[:64]):
+        s.last_tokens[i] = t
+    s.n_last = min(len(last), 64)
+    return s
+
+
+def sampler_candidates(logits, s: Sampler, max_k: int = 40):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    ids = np.zeros(max(max_k, 1), np.int32)
+    lgs = np.zeros(max(max_k, 1), np.float32)
+    k = lib().orc_sampler_candidates(logits.size, _p(logits), C.byref(s), _p(ids), _p(lgs), max_k)
+    return ids[:k].copy(), lgs[:k].copy()
+
+
+def sampler_pick(s: Sampler, ids, lgs, top_p: float) -> int:
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    lgs = np.ascontiguousarray(lgs, dtype=np.float32).copy()
+    return int(lib().orc_sampler_pick(C.byref(s), _p(ids), _p(lgs), ids.size, top_p))
 
 
 class MoeLayer(C.Structure):

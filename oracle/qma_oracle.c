@@ -878,3 +878,159 @@ void orc_quantize_q6k(const float *x, int64_t n, void *out)
         y[i].d = dh;
     }
 }
+
+/* ---------------------------------------------------------------------- */
+/* Sampler (src/sampler.c): repeat penalty, temperature, top-k candidates,  */
+/* top-p and the seeded draw.                                              */
+/* ---------------------------------------------------------------------- */
+
+/* xorshift64* step, sampler.c:9-14 */
+static uint64_t orc_rng_next(uint64_t *s)
+{
+    *s ^= *s >> 12;
+    *s ^= *s << 25;
+    *s ^= *s >> 27;
+    return *s * 0x2545F4914F6CDD1DULL;
+}
+
+typedef struct {
+    float p;
+    int id;
+} orc_cand;
+
+/* descending by value; the order of equal values is qsort's (sampler.c:28-33) */
+static int orc_cand_cmp(const void *a, const void *b)
+{
+    const orc_cand *x = (const orc_cand *)a, *y = (const orc_cand *)b;
+    if (x->p > y->p) return -1;
+    if (x->p < y->p) return 1;
+    return 0;
+}
+
+static void orc_heap_down(orc_cand *c, int k, int j)
+{
+    for (;;) {
+        const int lc = 2 * j + 1, rc = lc + 1;
+        int mn = j;
+        if (lc < k && c[lc].p < c[mn].p) mn = lc;
+        if (rc < k && c[rc].p < c[mn].p) mn = rc;
+        if (mn == j) break;
+        const orc_cand t = c[j];
+        c[j] = c[mn];
+        c[mn] = t;
+        j = mn;
+    }
+}
+
+/* sampler_candidates, sampler.c:36-97: penalty per occurrence in
+   last_tokens, then logits / temp, then the k largest by a min-heap over
+   (logit, id) in index order, sorted descending. */
+int orc_sampler_candidates(int n_vocab, const float *logits, const orc_sampler *s, int *ids, float *lgs,
+                           int max_k)
+{
+    const int n = n_vocab;
+    const float *l = logits;
+    float *buf = NULL;
+    if (s->repeat_penalty != 1.0f || s->temp > 0.0f) {
+        buf = (float *)malloc(sizeof(float) * (size_t)n);
+        if (!buf) return 0;
+        memcpy(buf, logits, sizeof(float) * (size_t)n);
+        if (s->repeat_penalty != 1.0f) {
+            for (int i = 0; i < s->n_last; i++) {
+                const int id = s->last_tokens[i];
+                if (id >= 0 && id < n) {
+                    if (buf[id] < 0.0f) buf[id] *= s->repeat_penalty;
+                    else buf[id] /= s->repeat_penalty;
+                }
+            }
+        }
+        if (s->temp > 0.0f)
+            for (int i = 0; i < n; i++) buf[i] /= s->temp;
+        l = buf;
+    }
+    int k = s->top_k;
+    if (k < 1) k = 1;
+    if (k > n) k = n;
+    if (k > max_k) k = max_k;
+    orc_cand *c = (orc_cand *)malloc(sizeof(orc_cand) * (size_t)(k > 0 ? k : 1));
+    if (!c) {
+        free(buf);
+        return 0;
+    }
+    for (int i = 0; i < k; i++) {
+        c[i].p = l[i];
+        c[i].id = i;
+    }
+    for (int i = k / 2 - 1; i >= 0; i--) orc_heap_down(c, k, i);
+    for (int i = k; i < n; i++) {
+        if (l[i] > c[0].p) {
+            c[0].p = l[i];
+            c[0].id = i;
+            orc_heap_down(c, k, 0);
+        }
+    }
+    qsort(c, (size_t)k, sizeof(orc_cand), orc_cand_cmp);
+    for (int i = 0; i < k; i++) {
+        ids[i] = c[i].id;
+        lgs[i] = c[i].p;
+    }
+    free(c);
+    free(buf);
+    return k;
+}
+
+/* sampler_pick, sampler.c:100-134: masked candidates carry <= -1e29; greedy
+   at temp <= 0; softmax over the live candidates (double sum), top-p cut,
+   one xorshift64* draw, cumulative pick; the pick joins last_tokens (64). */
+int orc_sampler_pick(orc_sampler *s, const int *ids, float *lgs, int n, float top_p)
+{
+    if (n <= 0) return 0;
+    int first_live = -1;
+    for (int i = 0; i < n; i++)
+        if (lgs[i] > -1e29f) {
+            first_live = i;
+            break;
+        }
+    if (first_live < 0) return ids[0];
+    if (s->temp <= 0.0f) return ids[first_live];
+    float mx = lgs[first_live];
+    for (int i = first_live; i < n; i++)
+        if (lgs[i] > -1e29f && lgs[i] > mx) mx = lgs[i];
+    double z = 0.0;
+    for (int i = first_live; i < n; i++)
+        if (lgs[i] > -1e29f) {
+            const float p = expf(lgs[i] - mx);
+            lgs[i] = p;
+            z += p;
+        }
+    const float inv = (float)(1.0 / z);
+    for (int i = first_live; i < n; i++)
+        if (lgs[i] > -1e29f) lgs[i] *= inv;
+    float acc = 0.0f;
+    int kept = first_live;
+    for (int i = first_live; i < n; i++) {
+        if (lgs[i] <= -1e29f) continue;
+        acc += lgs[i];
+        kept = i + 1;
+        if (acc >= top_p) break;
+    }
+    const uint64_t r = orc_rng_next(&s->seed);
+    const float rv = (float)((r >> 11) * (1.0 / 9007199254740992.0));
+    float cum = 0.0f;
+    int pick = ids[kept - 1];
+    for (int i = first_live; i < kept; i++) {
+        if (lgs[i] <= -1e29f) continue;
+        cum += lgs[i];
+        if (rv < cum) {
+            pick = ids[i];
+            break;
+        }
+    }
+    if (s->n_last < 64) {
+        s->last_tokens[s->n_last++] = pick;
+    } else {
+        memmove(s->last_tokens, s->last_tokens + 1, 63 * sizeof(int));
+        s->last_tokens[63] = pick;
+    }
+    return pick;
+}

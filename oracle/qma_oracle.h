@@ -114,6 +114,20 @@ float    orc_moe_shared_gate(const float *wsh, const int8_t *xq,
 /* residual chain used by the layer-stack workload: x <- x + moe_l(x) */
 void     orc_moe_stack(const orc_moe_layer *layers, int n_layer, float *x);
 
+/* ---- sampler (sampler.c), state in the layout of sampler_t (qma.h:279-287) ---- */
+typedef struct {
+    uint64_t seed;
+    float    temp;
+    int      top_k;
+    float    top_p;
+    float    repeat_penalty;
+    int      last_tokens[64];
+    int      n_last;
+} orc_sampler;
+int      orc_sampler_candidates(int n_vocab, const float *logits, const orc_sampler *s,
+                                int *ids, float *lgs, int max_k);
+int      orc_sampler_pick(orc_sampler *s, const int *ids, float *lgs, int n, float top_p);
+
 /* ---- synthetic inputs (the build's own generator and quantizers) ---- */
 uint64_t orc_splitmix64(uint64_t *state);
 void     orc_fill_normal(uint64_t seed, int64_t n, float mean, float std, float *out);

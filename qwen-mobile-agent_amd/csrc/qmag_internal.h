@@ -48,6 +48,7 @@ enum WsSlot {
     WS_GRP,                         // grouped prefill: bucket counts/offsets, pair permutation
     WS_Y,                           // grouped prefill: per-pair down outputs
     WS_XMB,                         // grouped prefill: Q8_K(x) sub-block sums times the block scale
+    WS_SAMP,                        // sampler: per-chunk candidates and the merged list
     WS_COUNT
 };
 void *workspace(int slot, size_t bytes, int *status);

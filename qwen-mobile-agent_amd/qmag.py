@@ -66,6 +66,8 @@ SIGNATURES = {
     "qmag_gguf_upload_tensor": (C.c_int, [P, C.c_char_p, C.POINTER(P), C.POINTER(C.c_int), C.POINTER(C.c_int64)]),
     "qmag_gguf_upload_moe_layer": (C.c_int, [P, C.c_int, P]),
     "qmag_gguf_free_moe_layer": (C.c_int, [P]),
+    "qmag_sampler_candidates_dev": (C.c_int, [C.c_int, P, P, P, P, C.c_int]),
+    "qmag_sampler_sample_dev": (C.c_int, [C.c_int, P, P, C.c_int, C.c_float, P]),
     "qmag_synth_normal": (C.c_int, [C.c_uint64, C.c_size_t, C.c_float, C.c_float, P]),
     "qmag_synth_weights": (C.c_int, [C.c_uint64, C.c_size_t, C.c_float, C.c_int, P]),
     "qmag_quantize_dev": (C.c_int, [P, C.c_size_t, C.c_int, P]),
@@ -409,6 +411,43 @@ class ResidentLayer:
             b = getattr(self, k, None)
             if b is not None:
                 b.close()
+
+
+# --------------------------------------------------------------- sampler --
+
+class Sampler(C.Structure):
+    """qmag_sampler: the layout of sampler_t (qma.h:279-287)."""
+    _fields_ = [("seed", C.c_uint64), ("temp", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("last_tokens", C.c_int * 64), ("n_last", C.c_int)]
+
+    @classmethod
+    def init(cls, seed=0, temp=0.7, top_k=40, top_p=0.95, repeat_penalty=1.0, last=()):
+        """sampler_init (sampler.c:16-23) plus an optional token history."""
+        s = cls()
+        s.seed = seed if seed else 0x9E3779B97F4A7C15
+        s.temp, s.top_k, s.top_p, s.repeat_penalty = temp, top_k, top_p, repeat_penalty
+        for i, t in enumerate(list(last)[:64]):
+            s.last_tokens[i] = t
+        s.n_last = min(len(last), 64)
+        return s
+
+
+def sampler_candidates_dev(logits_ptr: int, n_vocab: int, s: Sampler, max_k: int = 40):
+    """sampler_candidates on device logits: (ids, values), k of each."""
+    ids = np.zeros(max_k, np.int32)
+    lgs = np.zeros(max_k, np.float32)
+    k = lib().qmag_sampler_candidates_dev(n_vocab, logits_ptr, C.addressof(s), ids.ctypes.data,
+                                          lgs.ctypes.data, max_k)
+    check(min(k, 0))
+    return ids[:k].copy(), lgs[:k].copy()
+
+
+def sampler_sample_dev(logits_ptr: int, n_vocab: int, s: Sampler, max_k: int = 40, top_p: float = None) -> int:
+    """sampler_candidates + sampler_pick on the device; s is updated."""
+    tok = C.c_int()
+    check(lib().qmag_sampler_sample_dev(n_vocab, logits_ptr, C.addressof(s), max_k,
+                                        s.top_p if top_p is None else top_p, C.byref(tok)))
+    return tok.value
 
 
 # ------------------------------------------------------------------ GGUF --

@@ -1,0 +1,138 @@
+"""Device sampling (qmag_sampler_candidates_dev / qmag_sampler_sample_dev,
+the sampler_candidates + sampler_pick pair of src/sampler.c:36-134 as
+agent.c:935-955 calls it) against the oracle's restatement on the same
+logits and sampler state.
+
+Bar: candidates bit-exact (ids and values) when the logits are distinct; with
+exact ties the values are still bit-exact and the device orders equal values
+by ascending id, where the reference's order among them follows its heap
+(checked as a set).  Picks, seeds and token histories equal step for step
+over generation-length sequences (the pick's expf is the correctly rounded
+one on both sides; a differing last bit could move a pick only if the draw
+fell within ~1e-7 of a cumulative boundary)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+V = 151936                       # the Qwen3.5 vocabulary (LM-head rows)
+
+
+def _state(qm, orc, **kw):
+    return qm.Sampler.init(**kw), orc.make_sampler(**kw)
+
+
+def _check_candidates(qm, orc, logits, kw, max_k):
+    sd, so = _state(qm, orc, **kw)
+    d = qm.DBuf.from_array(logits)
+    gi, gv = qm.sampler_candidates_dev(d.ptr, logits.size, sd, max_k)
+    oi, ov = orc.sampler_candidates(logits, so, max_k)
+    assert gi.size == oi.size
+    assert np.array_equal(gv.view(np.uint32), ov.view(np.uint32))
+    if np.unique(ov).size == ov.size and (ov.size == 0 or np.count_nonzero(_scaled(orc, logits, kw) == ov[-1]) == 1):
+        assert np.array_equal(gi, oi)
+    else:
+        for v in np.unique(ov):
+            assert set(gi[gv == v]) <= set(np.flatnonzero(_scaled(orc, logits, kw) == v))
+            assert set(oi[ov == v]) <= set(np.flatnonzero(_scaled(orc, logits, kw) == v))
+    # the device's rule among equal values: ascending id
+    for v in np.unique(gv):
+        ids = gi[gv == v]
+        assert list(ids) == sorted(ids)
+    return gi, gv
+
+
+def _scaled(orc, logits, kw):
+    """The logits after the penalty and the temperature (sampler.c:47-58),
+    used only to find which vocabulary positions share a candidate's value."""
+    l = logits.astype(np.float32).copy()
+    rp = np.float32(kw.get("repeat_penalty", 1.0))
+    if rp != 1:
+        for t in list(kw.get("last", ()))[:64]:
+            if 0 <= t < l.size:
+                l[t] = l[t] * rp if l[t] < 0 else l[t] / rp
+    temp = np.float32(kw.get("temp", 0.7))
+    if temp > 0:
+        l = l / temp
+    return l
+
+
+@pytest.mark.parametrize("temp,top_k,max_k,rp", [(1.0, 20, 40, 1.1), (0.7, 40, 40, 1.0), (0.0, 5, 40, 1.3),
+                                                 (1.0, 64, 64, 1.0), (1.0, 0, 40, 1.0), (1.3, 300, 64, 1.1)])
+def test_candidates_vs_oracle(qm, orc, temp, top_k, max_k, rp):
+    rng = np.random.default_rng(1000 + top_k)
+    logits = (rng.standard_normal(V) * 3).astype(np.float32)
+    top = np.argsort(-logits)[:8]
+    # history: repeats, ids in the first and last chunk, the current top
+    # ids, and ids out of range (skipped)
+    last = list(rng.integers(0, V, 30)) + [5, 5, 5, V - 1, V - 1, -1, V + 3] + [int(t) for t in top]
+    logits[5] = -2.0
+    logits[V - 1] = 9.5
+    kw = dict(temp=temp, top_k=top_k, repeat_penalty=rp, last=last)
+    gi, _ = _check_candidates(qm, orc, logits, kw, max_k)
+    assert gi.size == min(max(top_k, 1), max_k)
+
+
+@pytest.mark.parametrize("n", [1, 3, 63, 64, 1000, 1024, 4095, 4097, 8191, 127 * 4096])
+def test_candidates_vocab_edges(qm, orc, n):
+    """Ragged vocabularies: k clamps to n_vocab (sampler.c:63-66), the last
+    chunk is partial, the largest vocabulary the device merge takes."""
+    rng = np.random.default_rng(n)
+    logits = rng.standard_normal(n).astype(np.float32)
+    for top_k, max_k in ((40, 40), (64, 64), (1, 40)):
+        gi, _ = _check_candidates(qm, orc, logits, dict(temp=0.8, top_k=top_k, repeat_penalty=1.0), max_k)
+        assert gi.size == min(top_k, max_k, n)
+
+
+def test_candidates_ties(qm, orc):
+    """Logits on a coarse grid (thousands of exact ties): the values match
+    bit for bit, the device takes the lowest ids of the boundary value."""
+    rng = np.random.default_rng(3)
+    logits = np.round(rng.standard_normal(V) * 4).astype(np.float32)
+    gi, gv = _check_candidates(qm, orc, logits, dict(temp=0.0, top_k=40, repeat_penalty=1.0), 40)
+    boundary = gv[-1]
+    assert list(gi[gv == boundary]) == list(np.flatnonzero(logits == boundary)[:np.count_nonzero(gv == boundary)])
+
+
+def test_candidates_rejects(qm):
+    s = qm.Sampler.init(top_k=40)
+    d = qm.DBuf.from_array(np.zeros(127 * 4096 + 1, np.float32))
+    for n, mk in ((127 * 4096 + 1, 40), (1000, 0), (1000, 65), (0, 40)):
+        with pytest.raises(qm.QmagError, match="sampler"):
+            qm.sampler_candidates_dev(d.ptr, n, s, mk)
+
+
+@pytest.mark.parametrize("temp,top_k,top_p,rp", [(1.0, 20, 0.95, 1.1), (0.7, 40, 0.9, 1.0), (1.5, 64, 1.0, 1.3),
+                                                 (0.3, 20, 0.1, 1.1), (0.0, 20, 0.95, 1.1)])
+def test_sample_sequence_vs_oracle(qm, orc, temp, top_k, top_p, rp):
+    """A 200-token generation: each step fresh logits (with the sampled
+    tokens' logits raised, so the penalty matters), the device pair against
+    the oracle pair; tokens, seeds and histories equal at every step."""
+    rng = np.random.default_rng(int(temp * 10) + top_k)
+    kw = dict(seed=12345 + top_k, temp=temp, top_k=top_k, top_p=top_p, repeat_penalty=rp)
+    sd, so = _state(qm, orc, **kw)
+    max_k = 64 if top_k > 40 else 40
+    d = qm.DBuf(4 * V)
+    for step in range(200):
+        logits = (rng.standard_normal(V) * 2.5).astype(np.float32)
+        for t in list(so.last_tokens)[:so.n_last]:
+            logits[t] += 4.0
+        d.upload(logits)
+        gt = qm.sampler_sample_dev(d.ptr, V, sd, max_k, top_p)
+        oi, ov = orc.sampler_candidates(logits, so, max_k)
+        ot = orc.sampler_pick(so, oi, ov, top_p)
+        assert gt == ot, step
+        assert sd.seed == so.seed and sd.n_last == so.n_last, step
+        assert list(sd.last_tokens)[:sd.n_last] == list(so.last_tokens)[:so.n_last], step
+    if temp > 0:
+        assert sd.n_last == 64                  # the history window filled and slid
+
+
+def test_sample_all_masked(qm, orc):
+    """Every candidate at or below -1e29 after the temperature: no draw, the
+    first candidate (the device's lowest id among the equal values), the
+    state untouched -- the all-masked answer of sampler_pick."""
+    sd = qm.Sampler.init(seed=9, temp=0.7, top_k=20)
+    d = qm.DBuf.from_array(np.full(5000, -1e30, np.float32))
+    assert qm.sampler_sample_dev(d.ptr, 5000, sd, 40, 0.95) == 0
+    assert sd.seed == 9 and sd.n_last == 0
