@@ -282,6 +282,71 @@ int qmag_gguf_upload_tensor(const qmag_gguf *g, const char *name, void **dptr, i
 int qmag_gguf_upload_moe_layer(const qmag_gguf *g, int il, qmag_moe_layer *L);
 /* Free the device tensors of a layer filled by qmag_gguf_upload_moe_layer. */
 int qmag_gguf_free_moe_layer(qmag_moe_layer *L);
+/* The expert cache's fetch callback over an opened file (user = the
+   qmag_gguf *): the record of (layer, expert) copied from the mapping, as
+   expert_fetch (nn.c:1564-1595) preads it; -1 when the layer or expert does
+   not exist.  qmag_gguf_expert_record_bytes gives the largest layer's record
+   size (down types vary per layer, nn.c:1601-1605). */
+int qmag_gguf_fetch_expert(void *user, int layer, int expert, uint8_t *dst);
+int qmag_gguf_expert_record_bytes(const qmag_gguf *g, size_t *rec);
+
+/* ------------------------------------------------------------------------ */
+/* Expert paging: a bounded cache of expert records in HBM (the role of      */
+/* qma_ecache, src/ecache.h:95-123, for models larger than the device)       */
+/* ------------------------------------------------------------------------ */
+
+/* The reference's fetch callback type (qma_fetch_fn, ecache.h:29-32): fill
+   dst (host memory, rec_bytes) with the record of (layer, expert) -- gate,
+   up and down slabs back to back (expert_fetch, nn.c:1564-1595) -- and
+   return 0.  Called from the reader threads and the calling thread, so it
+   must be safe to enter concurrently. */
+typedef int (*qmag_fetch_fn)(void *user, int layer, int expert, uint8_t *dst);
+typedef struct qmag_ecache qmag_ecache;
+typedef struct {
+    uint64_t hits, misses, bytes_read, evictions, prefetched, spec_issued;
+    int n_slots;
+    size_t rec_bytes, slot_bytes;
+} qmag_ecache_counters;
+
+/* replaces qma_ecache_init (ecache.h:95-96): budget / rec_bytes slots of
+   device memory (at least 4; none when the budget holds no record), policy
+   0 LFRU, 1 LRU.  The cache is allocated by the library (*c). */
+int qmag_ecache_init(qmag_ecache **c, size_t budget_bytes, size_t rec_bytes, int policy);
+/* replaces qma_ecache_free / qma_ecache_clear (ecache.h:97-98) */
+void qmag_ecache_free(qmag_ecache *c);
+void qmag_ecache_clear(qmag_ecache *c);
+/* replaces qma_ecache_get (ecache.h:100-105): the record's DEVICE address,
+   reading it through fetch on a miss or waiting for a read a hint started;
+   NULL on failure.  The bytes are in place when it returns; they stay valid
+   for work queued on the library stream before the next get. */
+const uint8_t *qmag_ecache_get(qmag_ecache *c, int layer, int expert, qmag_fetch_fn fetch, void *user);
+/* replaces qma_ecache_hold / qma_ecache_release (ecache.h:107-114): held
+   records stay valid for work queued before the release. */
+const uint8_t *qmag_ecache_hold(qmag_ecache *c, int layer, int expert, qmag_fetch_fn fetch, void *user);
+void qmag_ecache_release(qmag_ecache *c);
+/* replaces qma_ecache_io_start / _io_stop (ecache.h:116-123): nthreads
+   (<= 8) reader threads, each with pinned staging; depth reads in flight. */
+int qmag_ecache_io_start(qmag_ecache *c, qmag_fetch_fn fetch, void *user, int nthreads, int depth);
+void qmag_ecache_io_stop(qmag_ecache *c);
+/* replaces qma_ecache_hint / qma_ecache_prefetch (ecache.h:125-134) */
+void qmag_ecache_hint(qmag_ecache *c, int layer, const int *ids, int n);
+void qmag_ecache_prefetch(qmag_ecache *c, int layer, const int *ids, int n);
+/* No counterpart in the reference (its tests read the struct): wait until
+   every queued read has landed; the counters of qma_ecache; the slot that
+   holds (layer, expert) or -1; a slot's device address. */
+int qmag_ecache_drain(qmag_ecache *c);
+int qmag_ecache_stats(const qmag_ecache *c, qmag_ecache_counters *out);
+int qmag_ecache_slot_of(const qmag_ecache *c, int layer, int expert);
+const uint8_t *qmag_ecache_slot_ptr(const qmag_ecache *c, int slot);
+
+/* moe_ffn with the expert cache on (nn.c:553-571, 677-694): the router and
+   top-k on the device, the distinct selected experts hinted to the cache in
+   (token, slot) order, then per token its n_used records held, the expert
+   stages run on them, and released.  L's gate_exps/up_exps/down_exps are not
+   used (may be NULL); the router and the shared expert are resident.  One
+   host synchronisation per call (the selection). */
+int qmag_moe_ffn_paged_dev(const qmag_moe_layer *L, qmag_ecache *c, int il, qmag_fetch_fn fetch, void *user,
+                           const float *x, float *out, int T);
 
 /* ------------------------------------------------------------------------ */
 /* Sampling on the device (src/sampler.c), logits resident in HBM            */

@@ -76,6 +76,19 @@ def _declare(L):
     L.orc_fill_normal.argtypes = [C.c_uint64, C.c_int64, C.c_float, C.c_float, P]
     L.orc_sampler_candidates.restype = C.c_int
     L.orc_sampler_candidates.argtypes = [C.c_int, P, C.POINTER(Sampler), P, P, C.c_int]
+    L.orc_ecache_create.restype = P
+    L.orc_ecache_create.argtypes = [C.c_size_t, C.c_size_t, C.c_int, C.c_int, C.c_int]
+    L.orc_ecache_destroy.argtypes = [P]
+    L.orc_ecache_counters.argtypes = [P, P]
+    L.orc_ecache_io_start.argtypes = [P, C.c_int, C.c_int]
+    for f in ("orc_ecache_get", "orc_ecache_hold", "orc_ecache_lookup"):
+        getattr(L, f).restype = C.c_int
+        getattr(L, f).argtypes = [P, C.c_int, C.c_int]
+    L.orc_ecache_release.argtypes = [P]
+    L.orc_ecache_drain.argtypes = [P]
+    L.orc_ecache_clear.argtypes = [P]
+    L.orc_ecache_hint.argtypes = [P, C.c_int, P, C.c_int]
+    L.orc_ecache_prefetch.argtypes = [P, C.c_int, P, C.c_int]
     L.orc_sampler_pick.restype = C.c_int
     L.orc_sampler_pick.argtypes = [C.POINTER(Sampler), P, P, C.c_int, C.c_float]
     L.orc_quantize_q4k.argtypes = [P, C.c_int64, P]
@@ -110,6 +123,55 @@ def sampler_pick(s: Sampler, ids, lgs, top_p: float) -> int:
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     lgs = np.ascontiguousarray(lgs, dtype=np.float32).copy()
     return int(lib().orc_sampler_pick(C.byref(s), _p(ids), _p(lgs), ids.size, top_p))
+
+
+class ECacheModel:
+    """The expert cache policy of ecache.c (oracle/ecache_oracle.c): methods
+    return slot indices (-1 on failure) in place of record pointers."""
+    FIELDS = ("hits", "misses", "bytes_read", "evictions", "prefetched", "spec_issued", "n_slots")
+
+    def __init__(self, budget_bytes, rec_bytes, policy=0, n_layer=1 << 15, n_expert=1 << 16):
+        self.h = lib().orc_ecache_create(budget_bytes, rec_bytes, policy, n_layer, n_expert)
+        assert self.h
+
+    def io_start(self, nthreads, depth):
+        lib().orc_ecache_io_start(self.h, nthreads, depth)
+
+    def get(self, layer, expert):
+        return lib().orc_ecache_get(self.h, layer, expert)
+
+    def hold(self, layer, expert):
+        return lib().orc_ecache_hold(self.h, layer, expert)
+
+    def release(self):
+        lib().orc_ecache_release(self.h)
+
+    def hint(self, layer, ids):
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        lib().orc_ecache_hint(self.h, layer, _p(a), a.size)
+
+    def prefetch(self, layer, ids):
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        lib().orc_ecache_prefetch(self.h, layer, _p(a), a.size)
+
+    def drain(self):
+        lib().orc_ecache_drain(self.h)
+
+    def clear(self):
+        lib().orc_ecache_clear(self.h)
+
+    def lookup(self, layer, expert):
+        return lib().orc_ecache_lookup(self.h, layer, expert)
+
+    def stats(self):
+        out = np.zeros(7, np.uint64)
+        lib().orc_ecache_counters(self.h, _p(out))
+        return dict(zip(self.FIELDS, (int(v) for v in out)))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_ecache_destroy(self.h)
+            self.h = None
 
 
 class MoeLayer(C.Structure):

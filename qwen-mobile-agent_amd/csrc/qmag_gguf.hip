@@ -357,6 +357,50 @@ int qmag_gguf_upload_moe_layer(const qmag_gguf *g, int il, qmag_moe_layer *L)
     return QMAG_OK;
 }
 
+// One expert's record from the mapping: its gate, up and down slabs back to
+// back (the layout expert_fetch, nn.c:1564-1595, preads into the cache).
+static int expert_slabs(const qmag_gguf *g, int layer, int expert, const GgufTensor *t[3])
+{
+    static const char *names[] = {"ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"};
+    for (int i = 0; i < 3; i++) {
+        const std::string nm = "blk." + std::to_string(layer) + "." + names[i] + ".weight";
+        t[i] = find(g, nm);
+        if (!t[i] || t[i]->ne[2] <= 0) return -1;
+    }
+    if (expert < 0 || expert >= t[0]->ne[2] || t[1]->ne[2] != t[0]->ne[2] || t[2]->ne[2] != t[0]->ne[2]) return -1;
+    return 0;
+}
+
+int qmag_gguf_fetch_expert(void *user, int layer, int expert, uint8_t *dst)
+{
+    const qmag_gguf *g = (const qmag_gguf *)user;
+    const GgufTensor *t[3];
+    if (!g || !dst || layer < 0 || expert_slabs(g, layer, expert, t)) return -1;
+    for (int i = 0; i < 3; i++) {
+        const size_t slab = t[i]->nbytes / (size_t)t[i]->ne[2];
+        memcpy(dst, g->data + t[i]->off + (size_t)expert * slab, slab);
+        dst += slab;
+    }
+    return 0;
+}
+
+int qmag_gguf_expert_record_bytes(const qmag_gguf *g, size_t *rec)
+{
+    // the largest layer's record (nn.c:1601-1605): down types vary per layer
+    if (!g || !rec) return err(QMAG_ERR_ARG, "gguf: bad argument");
+    size_t best = 0;
+    for (int il = 0;; il++) {
+        const GgufTensor *t[3];
+        if (expert_slabs(g, il, 0, t)) break;
+        size_t r = 0;
+        for (int i = 0; i < 3; i++) r += t[i]->nbytes / (size_t)t[i]->ne[2];
+        if (r > best) best = r;
+    }
+    if (!best) return err(QMAG_ERR_ARG, "gguf: no blk.0 expert tensors");
+    *rec = best;
+    return QMAG_OK;
+}
+
 int qmag_gguf_free_moe_layer(qmag_moe_layer *L)
 {
     if (!L) return err(QMAG_ERR_ARG, "gguf: null layer");

@@ -85,7 +85,8 @@ int launch_f32dot(const float *x, const void *W, int n_in, int n_out, int T, int
                   hipStream_t s);
 int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const float *resid,
             hipStream_t s);
-int moe_check_layer(const qmag_moe_layer *L);
+// need_exps = false: the routed expert slabs may be null (paged experts)
+int moe_check_layer(const qmag_moe_layer *L, bool need_exps = true);
 
 // grouped prefill (qmag_prefill.hip)
 int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *logits, hipStream_t s);

@@ -14,6 +14,8 @@
 //                   optionally plus a residual                         nn.c:435-437, 468-472, 614-629
 #include <limits.h>
 
+#include <vector>
+
 #include "qmag_internal.h"
 
 namespace qmag {
@@ -196,6 +198,14 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
     }
 }
 
+// Routed experts addressed through per-slot record pointers (records of
+// the HBM expert cache: gate slab, up slab, down slab back to back) instead
+// of the layer's expert-major slabs; rec[0] == nullptr selects the slabs.
+struct ExpertRecs {
+    const uint8_t *rec[8];
+    unsigned long long gu;                  // bytes of one gate (= up) slab
+};
+
 // --------------------------------------------------------------- gate/up --
 // A wave holds R = 32/LPR row pairs: lanes [0,32) the gate rows, lanes
 // [32,64) the matching up rows.  After the per-row reduction the two halves
@@ -204,7 +214,7 @@ template <int NBE>
 __global__ __launch_bounds__(256) void gateup_kernel(const uint8_t *__restrict__ gate_exps,
                                                      const uint8_t *__restrict__ up_exps,
                                                      const uint8_t *__restrict__ gate_sh,
-                                                     const uint8_t *__restrict__ up_sh,
+                                                     const uint8_t *__restrict__ up_sh, const ExpertRecs recs,
                                                      const int *__restrict__ sel, int K, int F,
                                                      const int8_t *__restrict__ xq,
                                                      const float *__restrict__ xd,
@@ -228,7 +238,9 @@ __global__ __launch_bounds__(256) void gateup_kernel(const uint8_t *__restrict__
     const int base = (wave % steps_per_slot) * R * U;
 
     const uint8_t *mat;
-    if (slot < K) {
+    if (slot < K && recs.rec[0]) {
+        mat = recs.rec[slot] + (half ? recs.gu : 0);
+    } else if (slot < K) {
         const size_t slab = (size_t)F * RB;
         mat = (half ? up_exps : gate_exps) + (size_t)sel[slot] * slab;
     } else {
@@ -304,7 +316,7 @@ struct DownTask<QMAG_TYPE_Q6_K> {
 
 template <int NBF, int TD, int TDS>
 __global__ __launch_bounds__(256) void down_kernel(const uint8_t *__restrict__ down_exps,
-                                                   const uint8_t *__restrict__ down_sh,
+                                                   const uint8_t *__restrict__ down_sh, const ExpertRecs recs,
                                                    const int *__restrict__ sel,
                                                    const float *__restrict__ w,
                                                    const float *__restrict__ gs, int K, int N,
@@ -327,8 +339,8 @@ __global__ __launch_bounds__(256) void down_kernel(const uint8_t *__restrict__ d
     float acc = 0.0f;
     for (int k = 0; k < K; k++) {
         const size_t slab = (size_t)N * NBF * DownTask<TD>::BLOCK;
-        const uint8_t *blk = down_exps + (size_t)sel[k] * slab +
-                             ((size_t)rowc * NBF + ib) * DownTask<TD>::BLOCK;
+        const uint8_t *mat = recs.rec[0] ? recs.rec[k] + 2 * recs.gu : down_exps + (size_t)sel[k] * slab;
+        const uint8_t *blk = mat + ((size_t)rowc * NBF + ib) * DownTask<TD>::BLOCK;
         const float d = group_sum<LPR>(DownTask<TD>::dot(blk, hq + (size_t)k * F, hd + (size_t)k * NBF,
                                                          hs + (size_t)k * (F / 16), ib, q));
         acc = __fadd_rn(acc, __fmul_rn(w[k], d));
@@ -350,7 +362,7 @@ static bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (
 // per-token launch sequence below
 constexpr int GROUPED_MIN_T = 8;
 
-int moe_check_layer(const qmag_moe_layer *L)
+int moe_check_layer(const qmag_moe_layer *L, bool need_exps)
 {
     if (!L) return fail(QMAG_ERR_ARG, "moe: null layer");
     if (L->n_embd % QK_K || !pow2_in(L->n_embd / QK_K, 1, 16))
@@ -362,7 +374,7 @@ int moe_check_layer(const qmag_moe_layer *L)
         return fail(QMAG_ERR_ARG, "moe: n_used=%d", L->n_used);
     for (int t : {L->t_down_exps, L->t_down_shexp})
         if (t != QMAG_TYPE_Q4_K && t != QMAG_TYPE_Q6_K) return fail(QMAG_ERR_ARG, "moe: down type %d", t);
-    if (!L->gate_inp || !L->gate_exps || !L->up_exps || !L->down_exps || !L->gate_inp_shexp ||
+    if (!L->gate_inp || (need_exps && (!L->gate_exps || !L->up_exps || !L->down_exps)) || !L->gate_inp_shexp ||
         !L->gate_shexp || !L->up_shexp || !L->down_shexp)
         return fail(QMAG_ERR_ARG, "moe: null tensor pointer");
     return QMAG_OK;
@@ -403,7 +415,7 @@ static MoeWs g_last;
 static int g_last_K = 0;
 
 template <int NBE>
-static void launch_gateup(const qmag_moe_layer *L, const MoeWs &ws, int t, hipStream_t s)
+static void launch_gateup(const qmag_moe_layer *L, const MoeWs &ws, int t, const ExpertRecs &recs, hipStream_t s)
 {
     constexpr int TPR = 4 * NBE;
     constexpr int LPR = TPR < 32 ? TPR : 32;
@@ -413,21 +425,21 @@ static void launch_gateup(const qmag_moe_layer *L, const MoeWs &ws, int t, hipSt
     const int waves = steps * S;
     hipLaunchKernelGGL(gateup_kernel<NBE>, dim3((waves + 3) / 4), dim3(256), 0, s,
                        (const uint8_t *)L->gate_exps, (const uint8_t *)L->up_exps,
-                       (const uint8_t *)L->gate_shexp, (const uint8_t *)L->up_shexp,
+                       (const uint8_t *)L->gate_shexp, (const uint8_t *)L->up_shexp, recs,
                        ws.sel + (size_t)t * K, K, F, ws.xq + (size_t)t * N, ws.xd + (size_t)t * (N / QK_K),
                        ws.xs + (size_t)t * (N / 16), ws.h + (size_t)t * S * F);
 }
 
 template <int NBF, int TD, int TDS>
-static void launch_down3(const qmag_moe_layer *L, const MoeWs &ws, int t, const float *resid,
-                         float *out, hipStream_t s)
+static void launch_down3(const qmag_moe_layer *L, const MoeWs &ws, int t, const ExpertRecs &recs,
+                         const float *resid, float *out, hipStream_t s)
 {
     const int N = L->n_embd, F = L->n_ff, K = L->n_used, S = K + 1;
     constexpr int RPW = 64 / (4 * NBF);
     const int waves = (N + RPW - 1) / RPW;
     // one wave per workgroup: the grid is only N/RPW waves, spread it over CUs
     hipLaunchKernelGGL((down_kernel<NBF, TD, TDS>), dim3(waves), dim3(64), 0, s,
-                       (const uint8_t *)L->down_exps, (const uint8_t *)L->down_shexp,
+                       (const uint8_t *)L->down_exps, (const uint8_t *)L->down_shexp, recs,
                        ws.sel + (size_t)t * K, ws.w + (size_t)t * K, ws.gs + t, K, N,
                        ws.hq + (size_t)t * S * F, ws.hd + (size_t)t * S * (F / QK_K),
                        ws.hs + (size_t)t * S * (F / 16), resid ? resid + (size_t)t * N : nullptr,
@@ -435,14 +447,65 @@ static void launch_down3(const qmag_moe_layer *L, const MoeWs &ws, int t, const 
 }
 
 template <int NBF>
-static void launch_down2(const qmag_moe_layer *L, const MoeWs &ws, int t, const float *resid,
-                         float *out, hipStream_t s)
+static void launch_down2(const qmag_moe_layer *L, const MoeWs &ws, int t, const ExpertRecs &recs,
+                         const float *resid, float *out, hipStream_t s)
 {
     const bool r6 = L->t_down_exps == QMAG_TYPE_Q6_K, s6 = L->t_down_shexp == QMAG_TYPE_Q6_K;
-    if (r6 && s6) launch_down3<NBF, QMAG_TYPE_Q6_K, QMAG_TYPE_Q6_K>(L, ws, t, resid, out, s);
-    else if (r6) launch_down3<NBF, QMAG_TYPE_Q6_K, QMAG_TYPE_Q4_K>(L, ws, t, resid, out, s);
-    else if (s6) launch_down3<NBF, QMAG_TYPE_Q4_K, QMAG_TYPE_Q6_K>(L, ws, t, resid, out, s);
-    else launch_down3<NBF, QMAG_TYPE_Q4_K, QMAG_TYPE_Q4_K>(L, ws, t, resid, out, s);
+    if (r6 && s6) launch_down3<NBF, QMAG_TYPE_Q6_K, QMAG_TYPE_Q6_K>(L, ws, t, recs, resid, out, s);
+    else if (r6) launch_down3<NBF, QMAG_TYPE_Q6_K, QMAG_TYPE_Q4_K>(L, ws, t, recs, resid, out, s);
+    else if (s6) launch_down3<NBF, QMAG_TYPE_Q4_K, QMAG_TYPE_Q6_K>(L, ws, t, recs, resid, out, s);
+    else launch_down3<NBF, QMAG_TYPE_Q4_K, QMAG_TYPE_Q4_K>(L, ws, t, recs, resid, out, s);
+}
+
+// the per-token expert stages of the launch sequence: gate/up, Q8_K(h),
+// down + combine
+static int token_experts(const qmag_moe_layer *L, const MoeWs &ws, int t, const ExpertRecs &recs,
+                         const float *resid, float *out, hipStream_t s)
+{
+    const int N = L->n_embd, F = L->n_ff, K = L->n_used, S = K + 1;
+    prof_begin(PROF_GATEUP, s);
+    switch (N / QK_K) {
+    case 1: launch_gateup<1>(L, ws, t, recs, s); break;
+    case 2: launch_gateup<2>(L, ws, t, recs, s); break;
+    case 4: launch_gateup<4>(L, ws, t, recs, s); break;
+    case 8: launch_gateup<8>(L, ws, t, recs, s); break;
+    default: launch_gateup<16>(L, ws, t, recs, s); break;
+    }
+    prof_end(PROF_GATEUP, s);
+    prof_begin(PROF_HQUANT, s);
+    int st = launch_q8k_quant(ws.h + (size_t)t * S * F, S * (F / QK_K), ws.hq + (size_t)t * S * F,
+                              ws.hd + (size_t)t * S * (F / QK_K), ws.hs + (size_t)t * S * (F / 16), s);
+    prof_end(PROF_HQUANT, s);
+    if (st) return st;
+    prof_begin(PROF_DOWN, s);
+    switch (F / QK_K) {
+    case 1: launch_down2<1>(L, ws, t, recs, resid, out, s); break;
+    case 2: launch_down2<2>(L, ws, t, recs, resid, out, s); break;
+    default: launch_down2<4>(L, ws, t, recs, resid, out, s); break;
+    }
+    prof_end(PROF_DOWN, s);
+    return QMAG_OK;
+}
+
+// router and top-k (with Q8_K(x) and the shared gate) for T tokens
+static int route_tokens(const qmag_moe_layer *L, const float *x, int T, bool grouped, const MoeWs &ws,
+                        hipStream_t s)
+{
+    const int N = L->n_embd, E = L->n_expert, K = L->n_used;
+    prof_begin(PROF_ROUTER, s);
+    if (grouped) {
+        int st = launch_router_mfma(L, x, T, ws.logits, s);
+        if (st) return st;
+    } else {
+        hipLaunchKernelGGL(router_kernel, dim3((E * T + 3) / 4), dim3(256), 0, s, L->gate_inp,
+                           L->router_bias, x, N, E, T, ws.logits);
+    }
+    prof_end(PROF_ROUTER, s);
+    prof_begin(PROF_TOPK, s);
+    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(256), 0, s, ws.logits, x, L->gate_inp_shexp, N,
+                       E, K, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs, grouped ? ws.xmb : nullptr);
+    prof_end(PROF_TOPK, s);
+    return QMAG_OK;
 }
 
 int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const float *resid,
@@ -454,22 +517,10 @@ int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const fl
     MoeWs ws;
     st = moe_ws(L, T, ws);
     if (st) return st;
-    const int N = L->n_embd, F = L->n_ff, E = L->n_expert, K = L->n_used, S = K + 1;
+    const int K = L->n_used;
     const bool grouped = T >= GROUPED_MIN_T && option(QMAG_OPT_GROUPED);
-
-    prof_begin(PROF_ROUTER, s);
-    if (grouped) {
-        st = launch_router_mfma(L, x, T, ws.logits, s);
-        if (st) return st;
-    } else {
-        hipLaunchKernelGGL(router_kernel, dim3((E * T + 3) / 4), dim3(256), 0, s, L->gate_inp,
-                           L->router_bias, x, N, E, T, ws.logits);
-    }
-    prof_end(PROF_ROUTER, s);
-    prof_begin(PROF_TOPK, s);
-    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(256), 0, s, ws.logits, x, L->gate_inp_shexp, N,
-                       E, K, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs, grouped ? ws.xmb : nullptr);
-    prof_end(PROF_TOPK, s);
+    st = route_tokens(L, x, T, grouped, ws, s);
+    if (st) return st;
     if (grouped) {
         st = moe_grouped(L, T, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xmb, ws.h, ws.hq, ws.hd, ws.hs, resid, out,
                          s);
@@ -478,28 +529,10 @@ int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const fl
         g_last_K = K;
         return QMAG_OK;
     }
+    const ExpertRecs slabs = {};
     for (int t = 0; t < T; t++) {
-        prof_begin(PROF_GATEUP, s);
-        switch (N / QK_K) {
-        case 1: launch_gateup<1>(L, ws, t, s); break;
-        case 2: launch_gateup<2>(L, ws, t, s); break;
-        case 4: launch_gateup<4>(L, ws, t, s); break;
-        case 8: launch_gateup<8>(L, ws, t, s); break;
-        default: launch_gateup<16>(L, ws, t, s); break;
-        }
-        prof_end(PROF_GATEUP, s);
-        prof_begin(PROF_HQUANT, s);
-        st = launch_q8k_quant(ws.h + (size_t)t * S * F, S * (F / QK_K), ws.hq + (size_t)t * S * F,
-                              ws.hd + (size_t)t * S * (F / QK_K), ws.hs + (size_t)t * S * (F / 16), s);
-        prof_end(PROF_HQUANT, s);
+        st = token_experts(L, ws, t, slabs, resid, out, s);
         if (st) return st;
-        prof_begin(PROF_DOWN, s);
-        switch (F / QK_K) {
-        case 1: launch_down2<1>(L, ws, t, resid, out, s); break;
-        case 2: launch_down2<2>(L, ws, t, resid, out, s); break;
-        default: launch_down2<4>(L, ws, t, resid, out, s); break;
-        }
-        prof_end(PROF_DOWN, s);
     }
     QMAG_HIP(hipGetLastError());
     g_last = ws;
@@ -557,6 +590,65 @@ extern "C" int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, flo
 namespace qmag {
 void moe_note_sequence_ran() { g_last_fused = false; }
 }  // namespace qmag
+
+// moe_ffn with the expert cache on (nn.c:553-571, 677-694): route all T
+// tokens, hint the distinct selected experts in (token, slot) order, then per
+// token hold its n_used records, run the expert stages on them and release.
+extern "C" int qmag_moe_ffn_paged_dev(const qmag_moe_layer *L, qmag_ecache *c, int il, qmag_fetch_fn fetch,
+                                      void *user, const float *x, float *out, int T)
+{
+    int st = require_ready();
+    if (st) return st;
+    st = moe_check_layer(L, false);
+    if (st) return st;
+    if (!c || !x || !out || T <= 0 || il < 0) return fail(QMAG_ERR_ARG, "moe_paged: bad arguments");
+    qmag_ecache_counters cc;
+    st = qmag_ecache_stats(c, &cc);
+    if (st) return st;
+    const int N = L->n_embd, F = L->n_ff, K = L->n_used;
+    const size_t gu = (size_t)F * (N / QK_K) * Q4K_BYTES;
+    const size_t dn = (size_t)N * (F / QK_K) * (L->t_down_exps == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES);
+    if (cc.n_slots < 4 || cc.rec_bytes < 2 * gu + dn)
+        return fail(QMAG_ERR_ARG, "moe_paged: cache records of %zu bytes (%d slots) cannot hold a %zu-byte expert",
+                    cc.rec_bytes, cc.n_slots, 2 * gu + dn);
+    hipStream_t s = ctx().stream;
+    MoeWs ws;
+    st = moe_ws(L, T, ws);
+    if (st) return st;
+    g_last_fused = false;
+    st = route_tokens(L, x, T, false, ws, s);
+    if (st) return st;
+    std::vector<int> sel((size_t)T * K);
+    QMAG_HIP(hipMemcpyAsync(sel.data(), ws.sel, sizeof(int) * sel.size(), hipMemcpyDeviceToHost, s));
+    QMAG_HIP(hipStreamSynchronize(s));
+    std::vector<int> ids;
+    std::vector<char> seen((size_t)L->n_expert, 0);
+    for (int e : sel)
+        if (!seen[(size_t)e]) {
+            seen[(size_t)e] = 1;
+            ids.push_back(e);
+        }
+    qmag_ecache_hint(c, il, ids.data(), (int)ids.size());
+    for (int t = 0; t < T; t++) {
+        ExpertRecs recs = {};
+        recs.gu = gu;
+        for (int k = 0; k < K; k++) {
+            recs.rec[k] = qmag_ecache_hold(c, il, sel[(size_t)t * K + k], fetch, user);
+            if (!recs.rec[k]) {
+                qmag_ecache_release(c);
+                return fail(QMAG_ERR_ARG, "moe_paged: layer %d expert %d could not be read", il,
+                            sel[(size_t)t * K + k]);
+            }
+        }
+        st = token_experts(L, ws, t, recs, nullptr, out, s);
+        qmag_ecache_release(c);      // after the launches: later copies wait for them
+        if (st) return st;
+    }
+    QMAG_HIP(hipGetLastError());
+    g_last = ws;
+    g_last_K = K;
+    return QMAG_OK;
+}
 
 extern "C" int qmag_moe_last_stage(const float **logits, const int **sel, const float **w,
                                    const float **gs, const float **h)

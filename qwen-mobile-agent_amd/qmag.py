@@ -66,6 +66,23 @@ SIGNATURES = {
     "qmag_gguf_upload_tensor": (C.c_int, [P, C.c_char_p, C.POINTER(P), C.POINTER(C.c_int), C.POINTER(C.c_int64)]),
     "qmag_gguf_upload_moe_layer": (C.c_int, [P, C.c_int, P]),
     "qmag_gguf_free_moe_layer": (C.c_int, [P]),
+    "qmag_ecache_init": (C.c_int, [C.POINTER(P), C.c_size_t, C.c_size_t, C.c_int]),
+    "qmag_ecache_free": (None, [P]),
+    "qmag_ecache_clear": (None, [P]),
+    "qmag_ecache_get": (P, [P, C.c_int, C.c_int, P, P]),
+    "qmag_ecache_hold": (P, [P, C.c_int, C.c_int, P, P]),
+    "qmag_ecache_release": (None, [P]),
+    "qmag_ecache_io_start": (C.c_int, [P, P, P, C.c_int, C.c_int]),
+    "qmag_ecache_io_stop": (None, [P]),
+    "qmag_ecache_hint": (None, [P, C.c_int, P, C.c_int]),
+    "qmag_ecache_prefetch": (None, [P, C.c_int, P, C.c_int]),
+    "qmag_ecache_drain": (C.c_int, [P]),
+    "qmag_ecache_stats": (C.c_int, [P, P]),
+    "qmag_ecache_slot_of": (C.c_int, [P, C.c_int, C.c_int]),
+    "qmag_ecache_slot_ptr": (P, [P, C.c_int]),
+    "qmag_moe_ffn_paged_dev": (C.c_int, [P, P, C.c_int, P, P, P, P, C.c_int]),
+    "qmag_gguf_fetch_expert": (C.c_int, [P, C.c_int, C.c_int, P]),
+    "qmag_gguf_expert_record_bytes": (C.c_int, [P, C.POINTER(C.c_size_t)]),
     "qmag_sampler_candidates_dev": (C.c_int, [C.c_int, P, P, P, P, C.c_int]),
     "qmag_sampler_sample_dev": (C.c_int, [C.c_int, P, P, C.c_int, C.c_float, P]),
     "qmag_synth_normal": (C.c_int, [C.c_uint64, C.c_size_t, C.c_float, C.c_float, P]),
@@ -413,6 +430,97 @@ class ResidentLayer:
                 b.close()
 
 
+# ---------------------------------------------------------- expert cache --
+
+FETCH_FN = C.CFUNCTYPE(C.c_int, P, C.c_int, C.c_int, P)
+
+
+class ECacheCounters(C.Structure):
+    _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("bytes_read", C.c_uint64),
+                ("evictions", C.c_uint64), ("prefetched", C.c_uint64), ("spec_issued", C.c_uint64),
+                ("n_slots", C.c_int), ("rec_bytes", C.c_size_t), ("slot_bytes", C.c_size_t)]
+
+
+class ECache:
+    """The HBM expert cache (qmag_ecache_*).  fetch: a C function pointer
+    (e.g. the GGUF fetch) or a Python callable (user, layer, expert, dst) ->
+    int, wrapped and kept alive here; user: a pointer value or None."""
+
+    def __init__(self, budget_bytes: int, rec_bytes: int, policy: int = 0, fetch=None, user=None):
+        h = P()
+        check(lib().qmag_ecache_init(C.byref(h), budget_bytes, rec_bytes, policy))
+        self.h = h.value
+        self.set_fetch(fetch, user)
+
+    def set_fetch(self, fetch, user=None):
+        if fetch is None or isinstance(fetch, int):
+            self._cb = None
+            self.fetch = fetch
+        else:
+            self._cb = fetch if isinstance(fetch, FETCH_FN) else FETCH_FN(fetch)
+            self.fetch = C.cast(self._cb, P).value
+        self.user = user
+
+    def io_start(self, nthreads: int, depth: int) -> None:
+        check(lib().qmag_ecache_io_start(self.h, self.fetch, self.user, nthreads, depth))
+
+    def io_stop(self) -> None:
+        lib().qmag_ecache_io_stop(self.h)
+
+    def get(self, layer: int, expert: int) -> int:
+        return lib().qmag_ecache_get(self.h, layer, expert, self.fetch, self.user) or 0
+
+    def hold(self, layer: int, expert: int) -> int:
+        return lib().qmag_ecache_hold(self.h, layer, expert, self.fetch, self.user) or 0
+
+    def release(self) -> None:
+        lib().qmag_ecache_release(self.h)
+
+    def hint(self, layer: int, ids) -> None:
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        lib().qmag_ecache_hint(self.h, layer, a.ctypes.data, a.size)
+
+    def prefetch(self, layer: int, ids) -> None:
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        lib().qmag_ecache_prefetch(self.h, layer, a.ctypes.data, a.size)
+
+    def drain(self) -> None:
+        check(lib().qmag_ecache_drain(self.h))
+
+    def clear(self) -> None:
+        lib().qmag_ecache_clear(self.h)
+
+    def stats(self) -> dict:
+        c = ECacheCounters()
+        check(lib().qmag_ecache_stats(self.h, C.byref(c)))
+        return {k: getattr(c, k) for k, _ in ECacheCounters._fields_}
+
+    def slot_of(self, layer: int, expert: int) -> int:
+        return lib().qmag_ecache_slot_of(self.h, layer, expert)
+
+    def slot_ptr(self, slot: int) -> int:
+        return lib().qmag_ecache_slot_ptr(self.h, slot) or 0
+
+    def moe_ffn_paged(self, layer: "MoeLayer", il: int, x_ptr: int, out_ptr: int, T: int) -> None:
+        check(lib().qmag_moe_ffn_paged_dev(C.byref(layer), self.h, il, self.fetch, self.user, x_ptr, out_ptr, T))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().qmag_ecache_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def gguf_fetch_fn() -> int:
+    """Address of qmag_gguf_fetch_expert, for ECache(fetch=...)."""
+    return C.cast(lib().qmag_gguf_fetch_expert, P).value
+
+
 # --------------------------------------------------------------- sampler --
 
 class Sampler(C.Structure):
@@ -483,6 +591,11 @@ class Gguf:
         L = MoeLayer()
         check(lib().qmag_gguf_upload_moe_layer(self.h, il, C.byref(L)))
         return L
+
+    def expert_record_bytes(self) -> int:
+        r = C.c_size_t()
+        check(lib().qmag_gguf_expert_record_bytes(self.h, C.byref(r)))
+        return r.value
 
     @staticmethod
     def free_moe_layer(L: MoeLayer) -> None:

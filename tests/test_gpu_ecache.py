@@ -1,0 +1,207 @@
+"""The HBM expert cache (qmag_ecache_*, the qma_ecache role of
+src/ecache.h:95-123) and the paged MoE layer (qmag_moe_ffn_paged_dev, moe_ffn
+with the cache on, nn.c:553-571, 677-694) on the GPU.
+
+* Policy: the same operation sequences on the device cache and on the
+  oracle's restatement of ecache.c give the same slot for every record and
+  the same counters after every operation.  The reference's reader threads
+  make in-flight timing part of its decisions; both sides drain the read
+  queue before each operation, where the two are defined to agree.
+* Records: every record handed out holds, in device memory, exactly the
+  gate/up/down slabs the GGUF file stores for that (layer, expert) -- read
+  through the GGUF fetch callback on reader threads and on the calling
+  thread, and through a Python callback.
+* The paged layer equals the resident launch sequence bit for bit (same
+  kernels, experts addressed through the cache's slots), across evictions
+  and with reader threads on.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import gguf_writer as gw
+from moe_fixtures import make_host_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def _write(orc, path, n_layer, N, F, E, K):
+    layers = [make_host_layer(orc, seed=300 + i, n_embd=N, n_ff=F, n_expert=E, n_used=K,
+                              t_down=(14 if i % 2 == 0 else 12)) for i in range(n_layer)]
+    gw.write_gguf(path, gw.qwen35moe_metadata(n_layer, N, E, K, F), gw.moe_model_tensors(layers))
+    return layers
+
+
+def _records(g, n_layer):
+    """Expected record bytes per (layer, expert): gate | up | down slabs."""
+    out = {}
+    for il in range(n_layer):
+        slabs = []
+        for nm in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"):
+            _, ne, data = g.tensor(f"blk.{il}.{nm}.weight")
+            slabs.append(data.reshape(ne[2], -1))
+        for e in range(slabs[0].shape[0]):
+            out[(il, e)] = np.concatenate([s[e] for s in slabs])
+    return out
+
+
+@pytest.fixture(scope="module")
+def small(orc, tmp_path_factory):
+    path = tmp_path_factory.mktemp("ec") / "small.gguf"
+    _write(orc, path, 2, 256, 256, 64, 4)
+    return path
+
+
+def _check_bytes(qm, recs, key, ptr, rec_bytes):
+    want = recs[key]
+    got = qm.d2h_ptr(ptr, np.uint8, want.size)
+    assert np.array_equal(got, want), key
+
+
+@pytest.mark.parametrize("n_slots,policy,nthreads", [(12, 0, 3), (9, 1, 1), (33, 0, 8)])
+def test_policy_matches_oracle(qm, orc, small, n_slots, policy, nthreads):
+    g = qm.Gguf(str(small))
+    rec = g.expert_record_bytes()
+    recs = _records(g, 2)
+    c = qm.ECache(n_slots * rec, rec, policy, fetch=qm.gguf_fetch_fn(), user=g.h)
+    m = orc.ECacheModel(n_slots * rec, rec, policy, n_layer=2, n_expert=64)
+    c.io_start(nthreads, 3)
+    m.io_start(nthreads, 3)
+    base = c.slot_ptr(0)
+    slot_bytes = c.stats()["slot_bytes"]
+    rng = np.random.default_rng(n_slots + policy)
+    try:
+        for step in range(1500):
+            c.drain()
+            m.drain()
+            r = rng.random()
+            layer = int(rng.integers(3))                   # layer 2 does not exist: reads fail
+            e = int(min(rng.zipf(1.2), 70)) - 1            # experts >= 64 do not exist
+            if r < 0.12:
+                ids = rng.integers(0, 66, int(rng.integers(1, 10)))
+                c.hint(layer, ids)
+                m.hint(layer, ids)
+            elif r < 0.2:
+                ids = rng.integers(-1, 66, int(rng.integers(1, 5)))
+                c.prefetch(layer, ids)
+                m.prefetch(layer, ids)
+            elif r < 0.25:
+                c.release()
+                m.release()
+            else:
+                hold = r < 0.35
+                p = c.hold(layer, e) if hold else c.get(layer, e)
+                s = m.hold(layer, e) if hold else m.get(layer, e)
+                got = (p - base) // slot_bytes if p else -1
+                assert got == s, (step, layer, e)
+                if p:
+                    _check_bytes(qm, recs, (layer, e), p, rec)
+            assert c.stats()["hits"] == m.stats()["hits"], step
+            cs, ms = c.stats(), m.stats()
+            for k in orc.ECacheModel.FIELDS:
+                assert cs[k] == ms[k], (step, k)
+        c.drain()
+        m.drain()
+        for layer in range(3):
+            for e in range(70):
+                assert c.slot_of(layer, e) == m.lookup(layer, e), (layer, e)
+    finally:
+        c.close()
+        g.close()
+
+
+def test_python_fetch_callback(qm, orc, small):
+    """Any fetch callback works, including one that reads from elsewhere than
+    a GGUF mapping; records fetched by reader threads and by the calling
+    thread land intact."""
+    g = qm.Gguf(str(small))
+    rec = g.expert_record_bytes()
+    recs = _records(g, 2)
+    calls = []
+
+    def fetch(user, layer, expert, dst):
+        calls.append((layer, expert))
+        b = recs.get((layer, expert))
+        if b is None:
+            return -1
+        C.memmove(dst, b.ctypes.data, b.size)
+        return 0
+
+    c = qm.ECache(6 * rec, rec, fetch=fetch)
+    try:
+        p = c.get(1, 5)                                   # synchronous read, calling thread
+        _check_bytes(qm, recs, (1, 5), p, rec)
+        assert c.get(1, 99) == 0 and c.stats()["misses"] == 2
+        c.io_start(2, 2)
+        c.hint(0, [3, 4, 6, 7])                          # capped at 6 / 4 = 1 id
+        c.drain()
+        for e in (3, 4):
+            _check_bytes(qm, recs, (0, e), c.get(0, e), rec)
+        assert (0, 3) in calls and (1, 99) in calls
+    finally:
+        c.close()
+        g.close()
+
+
+def test_paged_layer_equals_resident(qm, orc, tmp_path):
+    """Two qwen35moe-shaped layers (hidden 2048, expert ff 512, 16 experts,
+    top-8; Q6_K then Q4_K down) from a GGUF: the paged layer, its experts
+    read into a 12-slot cache (evictions on nearly every token), equals the
+    resident launch sequence bit for bit, synchronously and with 4 reader
+    threads."""
+    N, F, E, K = 2048, 512, 16, 8
+    path = tmp_path / "m.gguf"
+    _write(orc, path, 2, N, F, E, K)
+    g = qm.Gguf(str(path))
+    dev = [g.upload_moe_layer(il) for il in range(2)]
+    paged = []
+    for L in dev:                                       # router + shared resident, experts paged
+        P_ = qm.MoeLayer()
+        C.memmove(C.byref(P_), C.byref(L), C.sizeof(L))
+        P_.gate_exps = P_.up_exps = P_.down_exps = None
+        paged.append(P_)
+    rec = g.expert_record_bytes()
+    c = qm.ECache(12 * rec, rec, fetch=qm.gguf_fetch_fn(), user=g.h)
+    qm.set_fused(False)
+    try:
+        for threads in (0, 4):
+            if threads:
+                c.io_start(threads, 3)
+            for it in range(6):
+                T = 1 if it % 2 == 0 else 3
+                x = orc.fill_normal(900 + 10 * it + threads, T * N, 0.0, 1.0)
+                xb = qm.DBuf.from_array(x)
+                for il in range(2):
+                    want = qm.DBuf(4 * T * N)
+                    qm.moe_ffn_dev(dev[il], xb.ptr, want.ptr, T)
+                    w_stage = qm.moe_last_stage(E, K, F, T)
+                    got = qm.DBuf(4 * T * N)
+                    c.moe_ffn_paged(paged[il], il, xb.ptr, got.ptr, T)
+                    g_stage = qm.moe_last_stage(E, K, F, T)
+                    assert np.array_equal(got.download(np.uint32), want.download(np.uint32)), (threads, it, il)
+                    assert np.array_equal(g_stage["sel"], w_stage["sel"])
+        st = c.stats()
+        assert st["evictions"] > 0 and st["misses"] > 12
+    finally:
+        qm.set_fused(True)
+        c.close()
+        for L in dev:
+            qm.Gguf.free_moe_layer(L)
+        g.close()
+
+
+def test_paged_layer_rejects_small_records(qm, orc, small):
+    g = qm.Gguf(str(small))
+    L = g.upload_moe_layer(0)
+    rec = g.expert_record_bytes()
+    c = qm.ECache(8 * (rec - 256), rec - 256, fetch=qm.gguf_fetch_fn(), user=g.h)
+    x = qm.DBuf.from_array(np.ones(256, np.float32))
+    out = qm.DBuf(4 * 256)
+    try:
+        with pytest.raises(qm.QmagError, match="cannot hold"):
+            c.moe_ffn_paged(L, 0, x.ptr, out.ptr, 1)
+    finally:
+        c.close()
+        qm.Gguf.free_moe_layer(L)
+        g.close()
