@@ -9,7 +9,11 @@ sequence; weights (21.05 GB) and inputs are synthetic (seeded, generated in
 HBM) and resident before the timed region.
 
 Prints one JSON line.  value = tokens/s; HBM GB/s uses the algorithmic bytes
-of one token through 40 layers (818,544,640 B).
+of one token through 40 layers (818,544,640 B).  "aux" carries the other
+configurations, each with its CPU baseline (the oracle, timed on this host):
+C1 / C2 (the matmul seam at 2048x2048 Q4_K and the 151936x2048 Q6_K LM head),
+C3 (one layer per call), C5 (a 512-token prefill chunk), the engine's other
+projection shapes at T = 1, and device sampling over the vocabulary.
 """
 from __future__ import annotations
 
@@ -47,12 +51,58 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def cpu_info() -> dict:
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu": cpu}
+
+
+def _orc():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import orc
+    return orc
+
+
+def gpu_loop(fn, seconds: float, min_iters: int = 3) -> tuple[float, int]:
+    """Calls fn() back to back on the library stream for about `seconds`
+    (iteration count calibrated on a short first pass); returns (ms per
+    call from HIP events around the timed calls, calls)."""
+    qmag.sync()
+    timer = qmag.Timer(2, 3)
+    timer.start()
+    for _ in range(min_iters):
+        fn()
+    ms = timer.stop_ms() / min_iters
+    iters = max(min_iters, int(seconds * 1e3 / max(ms, 1e-3)))
+    timer.start()
+    for _ in range(iters):
+        fn()
+    return timer.stop_ms() / iters, iters
+
+
+def cpu_loop(fn, seconds: float, min_iters: int = 2) -> tuple[float, int]:
+    """Wall time per call of a CPU function run for about `seconds`."""
+    done = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and done >= min_iters:
+            return el / done, done
+
+
 def cpu_baseline(layers, seconds: float, n_layer_sample: int = 8):
     """Oracle (C restatement of the reference's q8k path, pool_run threads)
     on a bounded sample: the first n_layer_sample layers' bytes copied to the
     host, tokens decoded until `seconds` have elapsed; scaled to 40 layers."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import orc
+    orc = _orc()
     threads = min(os.cpu_count() or 1, 8)       # batch-1 MoE: 8 expert tasks (nn.c:162)
     hls = []
     for rl in layers[:n_layer_sample]:
@@ -62,29 +112,21 @@ def cpu_baseline(layers, seconds: float, n_layer_sample: int = 8):
                                  a["gate_shexp"], a["up_shexp"], a["down_shexp"], rl.t_down))
     orc.set_threads(threads)
     rng = np.random.default_rng(0)
-    done = 0
-    t0 = time.perf_counter()
-    while True:
-        x = rng.standard_normal(N_EMBD).astype(np.float32)
-        orc.moe_stack(hls, x)
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and done >= 2:
-            break
+    xs = [rng.standard_normal(N_EMBD).astype(np.float32) for _ in range(8)]
+    it = [0]
+
+    def one():
+        orc.moe_stack(hls, xs[it[0] % len(xs)])
+        it[0] += 1
+
+    sec, done = cpu_loop(one, seconds)
     orc.set_threads(1)
-    tok_s = done * n_layer_sample / N_LAYER / el
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    tok_s = n_layer_sample / N_LAYER / sec
+    ci = cpu_info()
     return {"value": tok_s, "unit": "tokens/s (40-layer equivalent)", "cores": threads,
-            "kind": "port",
-            "sample": f"{done} tokens x {n_layer_sample} of 40 layers ({el:.1f} s), scaled to 40 "
-                      f"layers; nproc={os.cpu_count()}, cpu={cpu}"}
+            "kind": "port", "us_per_layer_token": sec / n_layer_sample * 1e6,
+            "sample": f"{done} tokens x {n_layer_sample} of 40 layers ({done * sec:.1f} s), scaled to 40 "
+                      f"layers; nproc={ci['nproc']}, cpu={ci['cpu']}"}
 
 
 def matvec_bytes(n_in: int, n_out: int, wtype: int) -> int:
@@ -94,10 +136,13 @@ def matvec_bytes(n_in: int, n_out: int, wtype: int) -> int:
     return rb * n_out + 4 * n_in + (n_in + 4 * (n_in // 256) + 2 * (n_in // 16)) + 4 * n_out
 
 
-def aux_matvec(name: str, n_in: int, n_out: int, wtype: int, copies: int, iters: int) -> dict:
+def aux_matvec(name: str, n_in: int, n_out: int, wtype: int, copies: int, seconds: float,
+               cpu_seconds: float) -> dict:
     """Configs C1/C2: the matmul seam at T = 1 (one launch: the matvec
     quantises x to Q8_K itself), rotating over `copies` distinct weight
-    matrices so the working set exceeds the 256 MB last-level cache."""
+    matrices so the working set exceeds the 256 MB last-level cache; the CPU
+    baseline is the oracle's matmul (mm_worker rows over min(nproc, 16)
+    pool threads, nn.c:276-303) on the first copy's bytes."""
     rb = n_in // 256 * (144 if wtype == 12 else 210)
     Ws = [qmag.DBuf(rb * n_out) for _ in range(copies)]
     for i, w in enumerate(Ws):
@@ -105,60 +150,144 @@ def aux_matvec(name: str, n_in: int, n_out: int, wtype: int, copies: int, iters:
     x = qmag.DBuf(4 * n_in)
     qmag.synth_normal(0xC1, n_in, 0.0, 1.0, x.ptr)
     out = qmag.DBuf(4 * n_out)
-    for w in Ws:
-        qmag.matmul_dev(x, w, n_in, n_out, 1, wtype, out)
-    qmag.sync()
-    timer = qmag.Timer(2, 3)
-    timer.start()
-    for _ in range(iters):
+
+    def rotation():
         for w in Ws:
             qmag.matmul_dev(x, w, n_in, n_out, 1, wtype, out)
-    ms = timer.stop_ms()
+
+    rotation()
+    ms, iters = gpu_loop(rotation, seconds)
     calls = iters * copies
     qmag.prof_enable(True)
-    for w in Ws:
-        qmag.matmul_dev(x, w, n_in, n_out, 1, wtype, out)
+    rotation()
     qmag.sync()
     n_mv, t_mv = qmag.prof_read("matvec")
-    n_q, t_q = qmag.prof_read("q8k")
     qmag.prof_enable(False)
+    nbytes = matvec_bytes(n_in, n_out, wtype)
+    call_us = ms * 1e3 / copies
+    mv_us = t_mv * 1e3 / max(n_mv, 1)
+    res = {"config": name, "bytes_per_call": nbytes, "us_per_call": call_us, "calls": calls,
+           "gbps_per_call": nbytes / (call_us * 1e-6) / 1e9,
+           "frac_of_peak_per_call": nbytes / (call_us * 1e-6) / HBM_PEAK,
+           "matvec_kernel_us_event_pair": mv_us, "weight_copies": copies}
+    log(f"{name}: {call_us:.2f} us/call ({res['gbps_per_call']:.0f} GB/s, "
+        f"{100 * res['frac_of_peak_per_call']:.1f}% of peak), event-pair kernel {mv_us:.2f} us")
+    if cpu_seconds > 0:
+        orc = _orc()
+        W0 = Ws[0].download(np.uint8)
+        xh = x.download(np.float32)
+        threads = min(os.cpu_count() or 1, 16)
+        orc.set_threads(threads)
+        sec, done = cpu_loop(lambda: orc.matmul_q8k(xh, W0, n_in, n_out, 1, wtype), cpu_seconds)
+        orc.set_threads(1)
+        ci = cpu_info()
+        res["cpu_baseline"] = {"us_per_call": sec * 1e6, "gbps": nbytes / sec / 1e9, "cores": threads,
+                               "kind": "port", "sample": f"{done} calls, nproc={ci['nproc']}, cpu={ci['cpu']}"}
+        log(f"{name} cpu: {sec * 1e6:.0f} us/call on {threads} threads")
     for w in Ws:
         w.close()
-    nbytes = matvec_bytes(n_in, n_out, wtype)
-    call_us = ms * 1e3 / calls
-    mv_us = t_mv * 1e3 / max(n_mv, 1)
-    res = {"config": name, "bytes_per_call": nbytes, "us_per_call": call_us,
-           "gbps_per_call": nbytes / (call_us * 1e-6) / 1e9,
-           "matvec_kernel_us": mv_us, "q8k_kernel_us": t_q * 1e3 / max(n_q, 1),
-           "matvec_kernel_gbps": rb * n_out / (mv_us * 1e-6) / 1e9,
-           "weight_copies": copies}
-    res["matvec_kernel_frac_of_peak"] = res["matvec_kernel_gbps"] * 1e9 / HBM_PEAK
-    log(f"{name}: {call_us:.2f} us/call ({res['gbps_per_call']:.0f} GB/s incl. launches), "
-        f"matvec kernel {mv_us:.2f} us = {res['matvec_kernel_gbps']:.0f} GB/s")
     return res
 
 
-def aux_layer(cl, iters: int) -> dict:
+# the engine's other matmul() call sites at decode (T = 1), qma.h:186-199,
+# nn.c:2111-2113, 2162, 2165-2170, 2243
+PROJECTIONS = [("wq", 2048, 8192, 12), ("wk", 2048, 512, 12), ("wv_q6k", 2048, 512, 14),
+               ("wo", 4096, 2048, 12), ("wqkv_q6k", 2048, 8192, 14), ("attn_gate", 2048, 4096, 12),
+               ("ssm_beta", 2048, 32, 12), ("ssm_out", 4096, 2048, 12)]
+
+
+def aux_projections(seconds: float) -> dict:
+    """Per-call time of each projection shape at T = 1, rotating over enough
+    weight copies to exceed the last-level cache (>= 512 MB per shape)."""
+    out = {}
+    for name, n_in, n_out, wtype in PROJECTIONS:
+        rb = n_in // 256 * (144 if wtype == 12 else 210)
+        copies = max(2, min(256, (512 << 20) // (rb * n_out) + 1))
+        Ws = [qmag.DBuf(rb * n_out) for _ in range(copies)]
+        for i, w in enumerate(Ws):
+            qmag.synth_weights(0xF200 + i, n_in * n_out, 0.02, wtype, w.ptr)
+        x = qmag.DBuf(4 * n_in)
+        qmag.synth_normal(0xF2, n_in, 0.0, 1.0, x.ptr)
+        y = qmag.DBuf(4 * n_out)
+
+        def rotation():
+            for w in Ws:
+                qmag.matmul_dev(x, w, n_in, n_out, 1, wtype, y)
+
+        rotation()
+        ms, _ = gpu_loop(rotation, seconds)
+        us = ms * 1e3 / copies
+        nb = matvec_bytes(n_in, n_out, wtype)
+        out[name] = {"n_in": n_in, "n_out": n_out, "wtype": wtype, "us_per_call": us,
+                     "gbps": nb / (us * 1e-6) / 1e9, "weight_copies": copies}
+        for w in Ws:
+            w.close()
+    log("projections: " + ", ".join(f"{k} {v['us_per_call']:.2f} us ({v['gbps']:.0f} GB/s)" for k, v in out.items()))
+    return out
+
+
+def aux_sampler(seconds: float, cpu_seconds: float) -> dict:
+    """Device sampling over the 151,936-entry vocabulary (the
+    sampler_candidates + sampler_pick pair, agent.c:935-955, top_k 20 of
+    max 40, temp 1.0, top_p 0.95, repeat penalty 1.1 over a 64-token
+    history): per call on the GPU (logits resident; the token id comes
+    back), and the oracle's pair on one host thread (the reference's
+    sampler is single-threaded)."""
+    V = 151936
+    logits = qmag.DBuf(4 * V)
+    qmag.synth_normal(0x5A, V, 0.0, 3.0, logits.ptr)
+    hist = list(range(100, 164))
+    s = qmag.Sampler.init(seed=1, temp=1.0, top_k=20, top_p=0.95, repeat_penalty=1.1, last=hist)
+    qmag.sampler_sample_dev(logits.ptr, V, s, 40)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds or n < 10:
+        qmag.sampler_sample_dev(logits.ptr, V, s, 40)
+        n += 1
+    gpu_us = (time.perf_counter() - t0) / n * 1e6
+    res = {"config": "sampler: 151,936 logits, top_k 20 (max 40), temp 1, top_p 0.95, repeat penalty 1.1",
+           "gpu_us_per_token": gpu_us, "gpu_calls": n,
+           "note": "host wall time per call including the launch of both kernels and the 16-byte readback"}
+    if cpu_seconds > 0:
+        orc = _orc()
+        lh = logits.download(np.float32)
+        so = orc.make_sampler(seed=1, temp=1.0, top_k=20, top_p=0.95, repeat_penalty=1.1, last=hist)
+
+        def one():
+            ids, lgs = orc.sampler_candidates(lh, so, 40)
+            orc.sampler_pick(so, ids, lgs, 0.95)
+
+        sec, done = cpu_loop(one, cpu_seconds)
+        res["cpu_baseline"] = {"us_per_token": sec * 1e6, "cores": 1, "kind": "port", "sample": f"{done} calls"}
+    log(f"sampler: gpu {gpu_us:.1f} us/token" +
+        (f", cpu {res['cpu_baseline']['us_per_token']:.0f} us/token" if "cpu_baseline" in res else ""))
+    return res
+
+
+def aux_layer(cl, seconds: float, cpu_us_per_layer: float | None) -> dict:
     """Config C3: one MoE layer per call (T = 1, qmag_moe_ffn_dev), rotating
-    over the 40 resident layers."""
+    over the 40 resident layers.  CPU baseline: the oracle's per layer-token
+    time from the C4 sample (8 expert tasks on min(nproc, 8) threads)."""
     x = qmag.DBuf(4 * N_EMBD)
     out = qmag.DBuf(4 * N_EMBD)
     qmag.synth_normal(0xC3, N_EMBD, 0.0, 1.0, x.ptr)
-    for c in cl:
-        qmag.moe_ffn_dev(c, x.ptr, out.ptr, 1)
-    qmag.sync()
-    timer = qmag.Timer(2, 3)
-    timer.start()
-    for _ in range(iters):
+
+    def rotation():
         for c in cl:
             qmag.moe_ffn_dev(c, x.ptr, out.ptr, 1)
-    ms = timer.stop_ms()
-    us = ms * 1e3 / (iters * len(cl))
+
+    rotation()
+    ms, _ = gpu_loop(rotation, seconds)
+    us = ms * 1e3 / len(cl)
     res = {"config": "C3: one qwen35moe MoE FFN layer, batch-1 decode, one call per layer "
                      "rotating over 40 resident layers",
            "bytes_per_call": LAYER_TOKEN_BYTES, "us_per_call": us,
            "gbps": LAYER_TOKEN_BYTES / (us * 1e-6) / 1e9}
     res["frac_of_peak"] = res["gbps"] * 1e9 / HBM_PEAK
+    if cpu_us_per_layer:
+        res["cpu_baseline"] = {"us_per_call": cpu_us_per_layer, "kind": "port",
+                               "cores": min(os.cpu_count() or 1, 8),
+                               "sample": "per layer-token time of the C4 CPU sample"}
     log(f"C3 layer: {us:.2f} us/call, {res['gbps']:.0f} GB/s")
     return res
 
@@ -166,7 +295,7 @@ def aux_layer(cl, iters: int) -> dict:
 INT8_PEAK = 5.03e15       # dense int8 MFMA op/s, 256 CU x 2.4 GHz x 8192
 
 
-def aux_prefill(T: int = 512, n_layers: int = 3, iters: int = 5) -> dict:
+def aux_prefill(seconds: float, cpu_seconds: float, T: int = 512, n_layers: int = 3) -> dict:
     """Config C5: one MoE layer over a 512-token prefill chunk (grouped
     int8-MFMA expert GEMM), router logits skewed by a seeded per-expert bias
     ~N(0,1); rotating over n_layers layers so one layer's experts are not
@@ -180,20 +309,37 @@ def aux_prefill(T: int = 512, n_layers: int = 3, iters: int = 5) -> dict:
         qmag.moe_ffn_dev(rl.c, x.ptr, out.ptr, T)
         st = qmag.moe_last_stage(N_EXPERT, N_USED, N_FF, n_tok=T)
         distinct.append(len(np.unique(st["sel"])))
-    qmag.sync()
-    timer = qmag.Timer(2, 3)
-    timer.start()
-    for _ in range(iters):
+    def rotation():
         for rl in rls:
             qmag.moe_ffn_dev(rl.c, x.ptr, out.ptr, T)
-    ms = timer.stop_ms()
-    us = ms * 1e3 / (iters * n_layers)
+
+    ms, _ = gpu_loop(rotation, seconds)
+    us = ms * 1e3 / n_layers
     qmag.prof_enable(True)
     for rl in rls:
         qmag.moe_ffn_dev(rl.c, x.ptr, out.ptr, T)
     qmag.sync()
     kern = {k: qmag.prof_read(k) for k in ("router", "topk", "group", "gateup", "hquant", "down", "combine")}
     qmag.prof_enable(False)
+    cpu = None
+    if cpu_seconds > 0:
+        # the oracle's moe_ffn over the same chunk: T * 8 (token, expert)
+        # tasks on min(nproc, 16) pool threads (nn.c:576-612)
+        orc = _orc()
+        a = rls[0].host_arrays()
+        hl = orc.HostLayer(N_EMBD, N_FF, N_EXPERT, N_USED, a["gate_inp"], a["gate_exps"], a["up_exps"],
+                           a["down_exps"], rls[0].t_down, a["gate_inp_shexp"], a["gate_shexp"], a["up_shexp"],
+                           a["down_shexp"], rls[0].t_down, router_bias=a["router_bias"])
+        xh = x.download(np.float32)
+        threads = min(os.cpu_count() or 1, 16)
+        orc.set_threads(threads)
+        sec, done = cpu_loop(lambda: orc.moe_ffn(hl, xh, T), cpu_seconds, min_iters=1)
+        orc.set_threads(1)
+        ci = cpu_info()
+        cpu = {"us_per_layer": sec * 1e6, "tokens_per_s": T / sec, "cores": threads, "kind": "port",
+               "sample": f"{done} x one {T}-token layer ({T * N_USED} pair tasks); nproc={ci['nproc']}, "
+                         f"cpu={ci['cpu']}"}
+        log(f"C5 cpu: {sec * 1e3:.0f} ms/layer on {threads} threads")
     for rl in rls:
         rl.close()
     n_pairs = T * N_USED
@@ -213,19 +359,26 @@ def aux_prefill(T: int = 512, n_layers: int = 3, iters: int = 5) -> dict:
            "per_kernel_note": "HIP event pair around each launch on the library stream, one extra pass; "
                               "each pair adds a few us of its own, so short kernels read high (a kernel "
                               "trace gives their own durations; the sum exceeds us_per_layer)",
-           "gemm_kernels_mfma_frac": ops / (gemm_us * 1e-6) / INT8_PEAK if gemm_us else None}
+           "gemm_kernels_mfma_frac": ops / (gemm_us * 1e-6) / INT8_PEAK if gemm_us else None,
+           "cpu_baseline": cpu}
     log(f"C5 prefill: {us:.1f} us/layer ({res['tokens_per_s']:.0f} tok/s), {d:.0f} distinct experts, "
         f"int8 {res['mfma_tops']:.1f} TOP/s ({100 * res['mfma_frac_of_peak']:.1f}% of peak), "
         f"weights {res['hbm_gbps']:.0f} GB/s; kernels " + ", ".join(f"{k} {v:.1f}" for k, v in per_k.items()))
     return res
 
 
+AUX_LEGS = ("c1", "c2", "c3", "c5", "projections", "sampler")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU-baseline sample length of the headline (C4); the other CPU legs take a quarter")
+    ap.add_argument("--aux-seconds", type=float, default=1.5,
+                    help="GPU time per auxiliary configuration")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--tokens", type=int, default=N_TOK)
     ap.add_argument("--decode", choices=("fused", "sequence"), default="fused",
@@ -235,9 +388,16 @@ def main() -> int:
     ap.add_argument("--probe-copy-mb", type=int, default=0,
                     help="after the run, one device-to-device copy of this many MiB between two "
                          "fresh buffers: a copy kernel of known size for scaling HBM counters")
+    ap.add_argument("--aux", default="c1,c2,c3,c5,projections,sampler",
+                    help="comma-separated auxiliary configurations to run (a profile of one of them "
+                         "names only its kernels)")
     ap.add_argument("--no-aux", action="store_true",
-                    help="skip the C1/C2 matvec and C3 single-layer measurements")
+                    help="skip the auxiliary configurations (C1, C2, C3, C5, projections, sampler)")
     args = ap.parse_args()
+    unknown = [a for a in args.aux.split(",") if a and a not in AUX_LEGS]
+    if unknown:
+        print(f"unknown --aux entries {unknown}; known: {list(AUX_LEGS)}", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(this build runs on a single MI355X; across GPUs the experts would shard by id, "
@@ -323,18 +483,26 @@ def main() -> int:
         del src, dst
         log(f"probe copy of {args.probe_copy_mb} MiB done")
 
-    aux = None
-    if not args.no_aux:
-        aux = {"c1": aux_matvec("C1: Q4_K matvec 2048x2048, matmul seam, T=1", 2048, 2048, 12, 128, 20),
-               "c2": aux_matvec("C2: Q6_K LM head 151936x2048, matmul seam, T=1", 2048, 151936, 14, 2, 20),
-               "c3": aux_layer(cl, 5),
-               "c5": aux_prefill()}
-
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
         cpu = cpu_baseline(layers, args.cpu_seconds)
         log(f"cpu baseline {cpu['value']:.3f} tok/s")
+
+    aux = None
+    if not args.no_aux:
+        cs = 0.0 if args.no_cpu else args.cpu_seconds / 4
+        legs = {
+            "c1": lambda: aux_matvec("C1: Q4_K matvec 2048x2048, matmul seam, T=1", 2048, 2048, 12, 128,
+                                     args.aux_seconds, cs),
+            "c2": lambda: aux_matvec("C2: Q6_K LM head 151936x2048, matmul seam, T=1", 2048, 151936, 14, 2,
+                                     args.aux_seconds, cs),
+            "c3": lambda: aux_layer(cl, args.aux_seconds, cpu["us_per_layer_token"] if cpu else None),
+            "c5": lambda: aux_prefill(args.aux_seconds, cs),
+            "projections": lambda: aux_projections(args.aux_seconds / 4),
+            "sampler": lambda: aux_sampler(args.aux_seconds / 2, cs / 2),
+        }
+        aux = {k: legs[k]() for k in args.aux.split(",") if k}
 
     line = {
         "metric": METRIC, "value": tok_s, "unit": "tokens/s", "n_gpus": 1,

@@ -10,6 +10,18 @@
 // steps before consuming any of them.  Row sums use DPP/permlane reductions.
 #include "qmag_internal.h"
 
+// Launch shape of the tiled matvec: wave steps of rows in flight per wave,
+// waves per CU the grid is capped at, threads per workgroup.
+#ifndef QMAG_MV_U
+#define QMAG_MV_U 2
+#endif
+#ifndef QMAG_MV_CAP
+#define QMAG_MV_CAP 32
+#endif
+#ifndef QMAG_MV_WG
+#define QMAG_MV_WG 256
+#endif
+
 namespace qmag {
 
 __global__ __launch_bounds__(256) void q8k_quant_kernel(const float *__restrict__ x, int nblocks,
@@ -102,7 +114,7 @@ struct RowTask<QMAG_TYPE_Q6_K> {
 // (bit-identical), after its first weight rows are requested -- one launch
 // per matvec instead of two.
 template <int WT, int NB, bool ONE_TOKEN, bool XF = false>
-__global__ __launch_bounds__(256) void matvec_kernel(const uint8_t *__restrict__ W,
+__global__ __launch_bounds__(QMAG_MV_WG) void matvec_kernel(const uint8_t *__restrict__ W,
                                                      const int8_t *__restrict__ xq,
                                                      const float *__restrict__ xd,
                                                      const int16_t *__restrict__ xsum,
@@ -114,7 +126,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(const uint8_t *__restrict__
     constexpr int LPR = TPR < 64 ? TPR : 64;    // lanes per row
     constexpr int TPL = TPR / LPR;              // tasks per lane
     constexpr int RPW = 64 / LPR;               // rows per wave step
-    constexpr int U = 2;                        // wave steps in flight
+    constexpr int U = QMAG_MV_U;                // wave steps in flight
     constexpr size_t RB = (size_t)NB * RT::BLOCK;
     constexpr int N_IN = NB * QK_K;
 
@@ -146,7 +158,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(const uint8_t *__restrict__
         __shared__ __align__(16) int16_t s_xs[N_IN / 16];
         load_rows(base0);                       // the weights are in flight during the quantisation
         const int wv = (int)(threadIdx.x >> 6);
-        for (int b = wv; b < NB; b += 4) {
+        for (int b = wv; b < NB; b += QMAG_MV_WG / 64) {
             const Q8Lane r = q8k_quant_lane(ldg4(xf + b * QK_K + 4 * lane));
             ((uint32_t *)(s_xq + b * QK_K))[lane] = r.packed;
             if (lane == 0) s_xd[b] = r.d;
@@ -189,19 +201,20 @@ static int launch_mv_nb(const int8_t *xq, const float *xd, const int16_t *xsum, 
     constexpr int TPR = 4 * NB;
     constexpr int LPR = TPR < 64 ? TPR : 64;
     constexpr int RPW = 64 / LPR;
-    const long groups = ((long)n_out + RPW * 2 - 1) / (RPW * 2);
-    const long cap = (long)(ctx().n_cu > 0 ? ctx().n_cu : 256) * 32;    // waves
+    constexpr int WPG = QMAG_MV_WG / 64;        // waves per workgroup
+    const long groups = ((long)n_out + RPW * QMAG_MV_U - 1) / (RPW * QMAG_MV_U);
+    const long cap = (long)(ctx().n_cu > 0 ? ctx().n_cu : 256) * QMAG_MV_CAP;    // waves
     const long waves = groups < cap ? groups : cap;
-    const int wgs = (int)((waves + 3) / 4);
+    const int wgs = (int)((waves + WPG - 1) / WPG);
     prof_begin(PROF_MATVEC, s);
     if (xf)
-        hipLaunchKernelGGL((matvec_kernel<WT, NB, true, true>), dim3(wgs), dim3(256), 0, s,
+        hipLaunchKernelGGL((matvec_kernel<WT, NB, true, true>), dim3(wgs), dim3(QMAG_MV_WG), 0, s,
                            (const uint8_t *)W, xq, xd, xsum, out, n_out, 1, xf);
     else if (T == 1)
-        hipLaunchKernelGGL((matvec_kernel<WT, NB, true>), dim3(wgs), dim3(256), 0, s,
+        hipLaunchKernelGGL((matvec_kernel<WT, NB, true>), dim3(wgs), dim3(QMAG_MV_WG), 0, s,
                            (const uint8_t *)W, xq, xd, xsum, out, n_out, T, nullptr);
     else
-        hipLaunchKernelGGL((matvec_kernel<WT, NB, false>), dim3(wgs), dim3(256), 0, s,
+        hipLaunchKernelGGL((matvec_kernel<WT, NB, false>), dim3(wgs), dim3(QMAG_MV_WG), 0, s,
                            (const uint8_t *)W, xq, xd, xsum, out, n_out, T, nullptr);
     prof_end(PROF_MATVEC, s);
     QMAG_HIP(hipGetLastError());

@@ -8,8 +8,10 @@ oracle on the same bytes:
 * the q8k entries at row lengths that are not powers of two (q8k.c:92 takes
   any whole number of super-blocks), and called from 8 host threads at once
   as the engine's pool does (nn.c:276-289, 652-706);
-* the matmul seam at the engine's other projection shapes (qma.h:196-199:
-  wq 2048 -> 8192, wk / wv 2048 -> 512, wo 4096 -> 2048; wv's type varies).
+* the matmul seam at the engine's other projection shapes (qma.h:186-199:
+  wq / wqkv 2048 -> 8192, attn_gate 2048 -> 4096, wk / wv 2048 -> 512,
+  ssm_beta / ssm_alpha 2048 -> 32, wo / ssm_out 4096 -> 2048; the types of
+  wv and wqkv vary).
 """
 import ctypes as C
 import threading
@@ -210,7 +212,10 @@ def test_compat_entries_concurrent_threads(qm, orc):
 
 @pytest.mark.parametrize("name,n_in,n_out,wtype", [
     ("wq", 2048, 8192, 12), ("wk", 2048, 512, 12), ("wv_q4k", 2048, 512, 12), ("wv_q6k", 2048, 512, 14),
-    ("wo", 4096, 2048, 12), ("wo_q6k", 4096, 2048, 14)])
+    ("wo", 4096, 2048, 12), ("wo_q6k", 4096, 2048, 14),
+    # the recurrent (gated delta net) layers' projections, qma.h:186-194
+    ("wqkv_q6k", 2048, 8192, 14), ("attn_gate", 2048, 4096, 12), ("ssm_beta", 2048, 32, 12),
+    ("ssm_out", 4096, 2048, 12)])
 def test_matmul_projection_shapes(qm, orc, name, n_in, n_out, wtype):
     """The other matmul() call sites of qma_eval (nn.c:2111-2113, 2162,
     2165-2170, 2243) at the engine's shapes (qma.h:196-199), T = 1 (decode)
