@@ -369,7 +369,7 @@ typedef struct qmag_sampler {
    temp > 0, and the k = clamp(top_k, 1, min(n_vocab, max_k)) largest values
    in descending order, ids and values copied to the host arrays ids[k],
    lgs[k] (agent.c:935 asks for 40).  Returns k (>= 1) or a negative status.  max_k <= 64,
-   n_vocab <= 520192.  Equal values are ordered by ascending id (the
+   n_vocab <= 524288.  Equal values are ordered by ascending id (the
    reference's order among exact ties follows its heap). */
 int qmag_sampler_candidates_dev(int n_vocab, const float *logits, const qmag_sampler *s, int *ids, float *lgs,
                                 int max_k);

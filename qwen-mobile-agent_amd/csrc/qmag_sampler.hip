@@ -7,16 +7,17 @@
 // over the live candidates with a double sum, the top-p cut, one xorshift64*
 // draw and the cumulative pick, and the pick's entry into last_tokens.
 //
-// Two launches.  cand_chunk_kernel: one workgroup per 4096 logits, one wave
-// per 1024 of them; each lane holds 16 (indices lane + 64m), sorts them once
-// (descending value, ascending index among equal values) and the wave takes
-// its top k by k picks, each a wave max over the lane heads; wave 0 then
-// merges the four waves' lists the same way.  cand_merge_kernel: one
-// workgroup stages the chunks' sorted lists in LDS and one wave merges them
-// by k picks over the list heads (each lane owns up to two lists), then, in
-// the sampling form, one lane makes the pick with the reference's
-// arithmetic.  About 2 * 64 picks of ~0.1 us for k = 64; the logits are read
-// once (0.6 MB for the Qwen vocabulary).
+// One launch of one workgroup per 4096 logits.  Each workgroup applies the
+// penalty and the temperature to its logits and selects its k largest by a
+// radix select over unique 64-bit keys (the value's order-preserving bits,
+// then the complemented index, so equal values order by ascending index):
+// eight-bit digits, an LDS histogram per digit, stopping as soon as the
+// boundary digit's group is wholly in.  The last workgroup to finish (a
+// device-scope counter) selects the k largest of all chunks' candidates the
+// same way, sorts them with a 64-lane bitonic network, and, in the sampling
+// form, makes the pick with the reference's arithmetic, the candidates one
+// per lane and the sequential sums as uniform loops over the lanes.  Results
+// are written straight to pinned host memory.
 //
 // Among exactly equal values the lower index comes first.  The reference
 // keeps its candidates in a min-heap and sorts them with qsort, so which of
@@ -31,25 +32,24 @@
 
 namespace qmag {
 
-constexpr int SAMP_WAVE_CHUNK = 1024;       // logits per wave in the first launch
-constexpr int SAMP_PER_LANE = SAMP_WAVE_CHUNK / 64;
-constexpr int SAMP_WAVES = 4;
-constexpr int SAMP_CHUNK = SAMP_WAVES * SAMP_WAVE_CHUNK;   // logits per workgroup
+constexpr int SAMP_CHUNK = 4096;            // logits per workgroup
+constexpr int SAMP_PER_THREAD = SAMP_CHUNK / 256;
 constexpr int SAMP_MAX_K = 64;
-constexpr int SAMP_LISTS_PER_LANE = 2;      // the merge handles up to 128 chunks
-// 127 chunks: the merge's lists (127 * 64 * 8 bytes) and its 512 bytes of
-// output staging fill exactly the 64 KiB of LDS a workgroup gets by default
-constexpr int SAMP_MAX_VOCAB = 127 * SAMP_CHUNK;    // 520,192
+constexpr int SAMP_MERGE_PER_THREAD = 32;   // the last workgroup's share of n_chunks * k
+constexpr int SAMP_MAX_CHUNKS = 256 * SAMP_MERGE_PER_THREAD / SAMP_MAX_K;   // 128
+constexpr int SAMP_MAX_VOCAB = SAMP_MAX_CHUNKS * SAMP_CHUNK;               // 524,288
 
+// the repeat penalty's distinct last-token ids with their occurrence counts
 struct SampParams {
     float temp;
     float repeat_penalty;
-    int n_last;
-    int last[64];
+    int n_uniq;
+    int uniq[64];
+    int count[64];
 };
 
-// order key: descending float order as ascending unsigned order; 0 marks an
-// element past the end, 1 a NaN (after every other value)
+// value order as unsigned order: larger key = larger value; NaN lowest of
+// the numbers' keys (1), 0 = no element
 __device__ __forceinline__ uint32_t samp_key(float v)
 {
     if (v != v) return 1u;
@@ -61,153 +61,144 @@ __device__ __forceinline__ float samp_val(uint32_t k)
 {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
-
-template <int W>
-__device__ __forceinline__ uint32_t group_max_u(uint32_t v)
+// unique selection key: value bits, then the complemented index
+__device__ __forceinline__ uint64_t samp_comp(uint32_t key, int id)
 {
-    if constexpr (W >= 2) v = max(v, (uint32_t)dpp_i<DPP_XOR1>((int)v));
-    if constexpr (W >= 4) v = max(v, (uint32_t)dpp_i<DPP_XOR2>((int)v));
-    if constexpr (W >= 8) v = max(v, (uint32_t)dpp_i<DPP_HALF_MIRROR>((int)v));
-    if constexpr (W >= 16) v = max(v, (uint32_t)dpp_i<DPP_MIRROR>((int)v));
-    if constexpr (W >= 32) {
-        auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-        v = max(p[0], p[1]);
-    }
-    if constexpr (W >= 64) {
-        auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-        v = max(p[0], p[1]);
+    return ((uint64_t)key << 32) | (uint32_t)~(uint32_t)id;
+}
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m)
+{
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// inclusive prefix sum over the 64 lanes of a wave
+__device__ __forceinline__ int wave_incl_scan(int v)
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(v, d);
+        v += lane >= d ? o : 0;
     }
     return v;
 }
 
-// one pick: the largest head key; among equal keys the lowest index.  Returns
-// whether this lane's head was picked.
-__device__ __forceinline__ bool samp_pick(uint32_t head, int head_id, uint32_t &m)
+// exclusive prefix sum over the workgroup's 256 threads; s_w: 4 ints
+__device__ __forceinline__ int wg_excl_scan(int v, int *s_w, int *total)
 {
-    m = group_max_u<64>(head);
-    bool me = head == m;
-    const unsigned long long bal = __ballot(me);
-    if (bal & (bal - 1)) {
-        const int best = group_min_i<64>(me ? head_id : INT_MAX);
-        me = me && head_id == best;
-    }
-    return me;
+    const int t = (int)threadIdx.x, w = t >> 6;
+    const int incl = wave_incl_scan(v);
+    if ((t & 63) == 63) s_w[w] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int i = 0; i < w; i++) base += s_w[i];
+    *total = s_w[0] + s_w[1] + s_w[2] + s_w[3];
+    __syncthreads();
+    return base + incl - v;
 }
 
-__global__ __launch_bounds__(256) void cand_chunk_kernel(const float *__restrict__ logits, int n, SampParams P, int k,
-                                                         uint32_t *__restrict__ ckey, int *__restrict__ cid)
+// Marks the `need` largest nonzero keys held across the workgroup (E per
+// thread; all keys distinct): after the call sel[j] is set for exactly
+// min(need, nonzero count) of them.  s_hist: 256 uints, s_info: 4 ints.
+template <int E>
+__device__ void wg_select(const uint64_t (&c)[E], int need, bool (&sel)[E], uint32_t *s_hist, int *s_info)
 {
-    __shared__ float4 s_v4[SAMP_CHUNK / 4];
-    __shared__ uint32_t s_key[SAMP_WAVES][64][SAMP_PER_LANE + 1];
-    __shared__ int s_id[SAMP_WAVES][64][SAMP_PER_LANE + 1];
-    __shared__ uint32_t s_wk[SAMP_WAVES][SAMP_MAX_K + 1];
-    __shared__ int s_wi[SAMP_WAVES][SAMP_MAX_K + 1];
-    float *s_v = (float *)s_v4;
-    const int t = (int)threadIdx.x, lane = lane_id(), w = t >> 6;
-    const int base = (int)blockIdx.x * SAMP_CHUNK;
+    const int t = (int)threadIdx.x;
+    uint64_t prefix = 0;
+    int L = 0;
+    for (int pass = 0; pass < 8 && need > 0; pass++) {
+        const int shift = 56 - 8 * pass;
+        s_hist[t] = 0;
+        __syncthreads();
 #pragma unroll
-    for (int m = 0; m < SAMP_CHUNK / 4 / 256; m++) {
-        const int i = base + 4 * (t + 256 * m);
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i + 3 < n) v = ldg4(logits + i);
-        else {
-            if (i < n) v.x = logits[i];
-            if (i + 1 < n) v.y = logits[i + 1];
-            if (i + 2 < n) v.z = logits[i + 2];
-        }
-        s_v4[t + 256 * m] = v;
-    }
-    __syncthreads();
-    // repeat penalty (sampler.c:47-55): the first occurrence of each
-    // last-token id applies every occurrence, in order
-    if (P.repeat_penalty != 1.0f && t < P.n_last) {
-        const int id = P.last[t];
-        bool first = true;
-        for (int j = 0; j < t; j++) first = first && P.last[j] != id;
-        if (first && id >= base && id < base + SAMP_CHUNK && id < n) {
-            float v = s_v[id - base];
-            for (int j = t; j < P.n_last; j++)
-                if (P.last[j] == id) v = v < 0.0f ? v * P.repeat_penalty : v / P.repeat_penalty;
-            s_v[id - base] = v;
-        }
-    }
-    __syncthreads();
-    uint32_t key[SAMP_PER_LANE];
-    int id[SAMP_PER_LANE];
+        for (int j = 0; j < E; j++)
+            if (c[j] && (L == 0 || (c[j] >> (64 - L)) == prefix))
+                atomicAdd(&s_hist[(uint32_t)(c[j] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (t < 64) {
+            // lane l owns bins 4l .. 4l+3; counts above a bin run from bin 255 down
+            const uint32_t h0 = s_hist[4 * t], h1 = s_hist[4 * t + 1], h2 = s_hist[4 * t + 2],
+                           h3 = s_hist[4 * t + 3];
+            const int local = (int)(h0 + h1 + h2 + h3);
+            const int incl = wave_incl_scan(local);
+            const int tot = __shfl(incl, 63);
+            int above = tot - incl;                       // bins of the lanes above
+            const uint32_t h[4] = {h0, h1, h2, h3};
 #pragma unroll
-    for (int m = 0; m < SAMP_PER_LANE; m++) {
-        const int i = w * SAMP_WAVE_CHUNK + lane + 64 * m;
-        float v = s_v[i];
-        if (P.temp > 0.0f) v = v / P.temp;                       // sampler.c:56-58
-        id[m] = base + i;
-        key[m] = base + i < n ? samp_key(v) : 0u;
-    }
-    // the lane's 16 in descending (key, -index) order: Batcher's odd-even
-    // merge sort, unrolled into 63 compare-exchanges on registers
-    auto cs = [&](int a, int b) {
-        const bool sw = key[b] > key[a] || (key[b] == key[a] && id[b] < id[a]);
-        const uint32_t ka = key[a], kb = key[b];
-        const int ia = id[a], ib = id[b];
-        key[a] = sw ? kb : ka;
-        key[b] = sw ? ka : kb;
-        id[a] = sw ? ib : ia;
-        id[b] = sw ? ia : ib;
-    };
-#pragma unroll
-    for (int p = 1; p < SAMP_PER_LANE; p <<= 1)
-#pragma unroll
-        for (int q = p; q >= 1; q >>= 1)
-#pragma unroll
-            for (int j = q % p; j + q < SAMP_PER_LANE; j += 2 * q)
-#pragma unroll
-                for (int i = 0; i < q; i++)
-                    if (i + j + q < SAMP_PER_LANE && (i + j) / (2 * p) == (i + j + q) / (2 * p)) cs(i + j, i + j + q);
-#pragma unroll
-    for (int m = 0; m < SAMP_PER_LANE; m++) {
-        s_key[w][lane][m] = key[m];
-        s_id[w][lane][m] = id[m];
-    }
-    s_key[w][lane][SAMP_PER_LANE] = 0u;          // sentinel past each list
-    s_id[w][lane][SAMP_PER_LANE] = INT_MAX;
-    // k picks over the lane heads (each lane reads only its own row)
-    {
-        int h = 0;
-        uint32_t head = key[0];
-        int head_id = id[0];
-        for (int p = 0; p < k; p++) {
-            uint32_t m;
-            const bool me = samp_pick(head, head_id, m);
-            if (me) {
-                s_wk[w][p] = head;
-                s_wi[w][p] = head_id;
-                h = min(h + 1, SAMP_PER_LANE);
-                head = s_key[w][lane][h];
-                head_id = s_id[w][lane][h];
+            for (int i = 3; i >= 0; i--) {
+                if (above < need && need <= above + (int)h[i]) {
+                    s_info[0] = 4 * t + i;
+                    s_info[1] = above;
+                    s_info[2] = (int)h[i];
+                }
+                above += (int)h[i];
+            }
+            if (t == 0 && tot < need) {                   // fewer candidates than asked: all of them
+                s_info[0] = -1;
+                s_info[1] = tot;
+                s_info[2] = 0;
             }
         }
+        __syncthreads();
+        const int b = s_info[0], above = s_info[1], cnt = s_info[2];
+        __syncthreads();
+        if (b < 0) {                                      // take every nonzero key
+            prefix = 0;
+            L = 0;
+            break;
+        }
+        need -= above;
+        prefix = (prefix << 8) | (uint64_t)b;
+        L += 8;
+        if (cnt == need) break;                           // the boundary group is wholly in
     }
-    if (lane == 0) {
-        s_wk[w][k] = 0u;
-        s_wi[w][k] = INT_MAX;
-    }
-    __syncthreads();
-    // wave 0 merges the four lists: lane j < 4 holds list j's head
-    if (w == 0) {
-        int h = 0;
-        uint32_t head = lane < SAMP_WAVES ? s_wk[lane][0] : 0u;
-        int head_id = lane < SAMP_WAVES ? s_wi[lane][0] : INT_MAX;
-        for (int p = 0; p < k; p++) {
-            uint32_t m;
-            const bool me = samp_pick(head, head_id, m);
-            if (me) {
-                ckey[(size_t)blockIdx.x * k + p] = head;
-                cid[(size_t)blockIdx.x * k + p] = head_id;
-                h = min(h + 1, k);
-                head = lane < SAMP_WAVES ? s_wk[lane][h] : 0u;
-                head_id = lane < SAMP_WAVES ? s_wi[lane][h] : INT_MAX;
-            }
+#pragma unroll
+    for (int j = 0; j < E; j++) {
+        if (!c[j]) {
+            sel[j] = false;
+        } else if (L == 0) {
+            sel[j] = true;
+        } else {
+            const uint64_t top = c[j] >> (64 - L);
+            sel[j] = top >= prefix;
         }
     }
+}
+
+// wg_select after a cheap pre-filter: the need-th largest of the threads'
+// own maxima is a lower bound on the need-th largest key (need threads hold
+// a key at least that large), so keys below it cannot be selected; the exact
+// selection then runs on the few that remain, with little contention on the
+// histogram bins.  s_m: 4 uint64.
+template <int E>
+__device__ void wg_topk(uint64_t (&c)[E], int need, bool (&sel)[E], uint32_t *s_hist, int *s_info, uint64_t *s_m)
+{
+    const int t = (int)threadIdx.x;
+    uint64_t m[1] = {0ull};
+#pragma unroll
+    for (int j = 0; j < E; j++) m[0] = c[j] > m[0] ? c[j] : m[0];
+    bool ms[1];
+    wg_select<1>(m, need, ms, s_hist, s_info);
+    // the bound: the smallest selected maximum
+    uint64_t lo = ms[0] ? m[0] : ~0ull;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const uint64_t o = shfl_xor64(lo, d);
+        lo = o < lo ? o : lo;
+    }
+    if ((t & 63) == 0) s_m[t >> 6] = lo;
+    __syncthreads();
+    uint64_t bound = s_m[0];
+    for (int w = 1; w < 4; w++) bound = s_m[w] < bound ? s_m[w] : bound;
+    // fewer than `need` threads hold keys: the bound would cut keys the
+    // selection needs, so keep every key
+    if (__syncthreads_count(m[0] != 0ull) < need) bound = 1ull;
+#pragma unroll
+    for (int j = 0; j < E; j++) c[j] = c[j] >= bound ? c[j] : 0ull;
+    wg_select<E>(c, need, sel, s_hist, s_info);
 }
 
 // the reference's xorshift64* (sampler.c:9-14)
@@ -219,135 +210,212 @@ __device__ __forceinline__ uint64_t samp_rng(uint64_t &s)
     return s * 0x2545F4914F6CDD1DULL;
 }
 
-// sampler_pick (sampler.c:100-134) over k candidates in descending order,
-// in one lane.  Returns the token; *drew = 1 if a draw was made (the seed
-// advanced and the token joins last_tokens), 0 for the greedy and the
-// all-masked answers.
-__device__ int samp_pick_token(const int *cid, const float *cval, int k, float temp, float top_p, uint64_t &seed,
-                               int *drew)
+__device__ __forceinline__ float readlane_f(float v, int i)
 {
-    float lg[SAMP_MAX_K];
-    for (int i = 0; i < k; i++) lg[i] = cval[i];
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+
+// sampler_pick (sampler.c:100-134) with candidate i in lane i (i < k, in
+// descending order); every lane returns the token.  *drew = 1 when a draw
+// was made (the seed advanced; the token joins last_tokens).
+__device__ int samp_pick_wave(float lg, int id, int k, float temp, float top_p, uint64_t &seed, int *drew)
+{
+    const int lane = lane_id();
     *drew = 0;
-    int first_live = -1;
-    for (int i = 0; i < k; i++)
-        if (lg[i] > -1e29f) {
-            first_live = i;
-            break;
-        }
-    if (first_live < 0) return cid[0];                      // all masked
-    if (temp <= 0.0f) return cid[first_live];               // greedy
-    float mx = lg[first_live];
+    const bool live = lane < k && lg > -1e29f;
+    const unsigned long long lv = __ballot(live);
+    const int id0 = __shfl(id, 0);
+    if (!lv) return id0;                                   // all masked
+    const int first_live = __ffsll(lv) - 1;
+    if (temp <= 0.0f) return __shfl(id, first_live);       // greedy: the best live one
+    float mx = live ? lg : -INFINITY;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+    // expf correctly rounded, through double (the device's expf is not)
+    const float e = live ? (float)exp((double)__fsub_rn(lg, mx)) : 0.0f;
+    double z = 0.0;                                        // summed in index order
     for (int i = first_live; i < k; i++)
-        if (lg[i] > -1e29f && lg[i] > mx) mx = lg[i];
-    double z = 0.0;
-    for (int i = first_live; i < k; i++)
-        if (lg[i] > -1e29f) {
-            // expf correctly rounded, through double (the device's own expf
-            // is not correctly rounded)
-            const float e = (float)exp((double)__fsub_rn(lg[i], mx));
-            lg[i] = e;
-            z += (double)e;
-        }
+        if ((lv >> i) & 1ull) z += (double)readlane_f(e, i);
     const float inv = (float)(1.0 / z);
-    for (int i = first_live; i < k; i++)
-        if (lg[i] > -1e29f) lg[i] = __fmul_rn(lg[i], inv);
+    const float p = __fmul_rn(e, inv);
     float acc = 0.0f;
     int kept = first_live;
     for (int i = first_live; i < k; i++) {
-        if (lg[i] <= -1e29f) continue;
-        acc = __fadd_rn(acc, lg[i]);
+        if (!((lv >> i) & 1ull)) continue;
+        acc = __fadd_rn(acc, readlane_f(p, i));
         kept = i + 1;
         if (acc >= top_p) break;
     }
     const uint64_t r = samp_rng(seed);
     const float rv = (float)((double)(r >> 11) * (1.0 / 9007199254740992.0));
     float cum = 0.0f;
-    int pick = cid[kept - 1];
+    int pick = kept - 1;
     for (int i = first_live; i < kept; i++) {
-        if (lg[i] <= -1e29f) continue;
-        cum = __fadd_rn(cum, lg[i]);
+        if (!((lv >> i) & 1ull)) continue;
+        cum = __fadd_rn(cum, readlane_f(p, i));
         if (rv < cum) {
-            pick = cid[i];
+            pick = i;
             break;
         }
     }
     *drew = 1;
-    return pick;
+    return __shfl(id, pick);
 }
 
-// out: ids[k], vals[k]; in the sampling form also res[0] = picked token,
-// res[1] = 1 if the pick drew, res[2..3] = the new seed (low, high)
-__global__ __launch_bounds__(256) void cand_merge_kernel(const uint32_t *__restrict__ ckey, const int *__restrict__ cid,
-                                                         int n_chunks, int k, int *__restrict__ ids,
-                                                         float *__restrict__ vals, int sample, uint64_t seed,
-                                                         float temp, float top_p, int *__restrict__ res)
+// out (pinned host memory): [0..63] ids, [64..127] values (float bits),
+// [128] token, [129] drew, [130..131] new seed (low, high), [132] = seq
+// once everything before it is visible to the host
+__global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ logits, int n, SampParams P, int k,
+                                                      int n_chunks, uint64_t *__restrict__ cand,
+                                                      unsigned *__restrict__ done, int sample, uint64_t seed,
+                                                      float top_p, int *__restrict__ out, int seq)
 {
-    extern __shared__ uint32_t s_dyn[];
-    uint32_t *s_key = s_dyn;                              // [n_chunks][k]
-    int *s_id = (int *)(s_dyn + (size_t)n_chunks * k);
-    __shared__ int s_oid[SAMP_MAX_K];
-    __shared__ float s_oval[SAMP_MAX_K];
-    for (int i = (int)threadIdx.x; i < n_chunks * k; i += (int)blockDim.x) {
-        s_key[i] = ckey[i];
-        s_id[i] = cid[i];
+    __shared__ float4 s_v4[SAMP_CHUNK / 4];
+    __shared__ uint32_t s_hist[256];
+    __shared__ int s_info[4], s_w[4];
+    __shared__ uint64_t s_win[SAMP_MAX_K];
+    __shared__ int s_last;
+    __shared__ uint64_t s_m[4];
+    float *s_v = (float *)s_v4;
+    const int t = (int)threadIdx.x;
+    const int base = (int)blockIdx.x * SAMP_CHUNK;
+#pragma unroll
+    for (int m = 0; m < SAMP_PER_THREAD / 4; m++) {
+        const int i = base + 4 * (t + 256 * m);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i + 3 < n) v = ldg4(logits + i);
+        else {
+            if (i < n) v.x = logits[i];
+            if (i + 1 < n) v.y = logits[i + 1];
+            if (i + 2 < n) v.z = logits[i + 2];
+        }
+        s_v4[t + 256 * m] = v;
     }
     __syncthreads();
-    if (threadIdx.x < 64) {
-        const int lane = lane_id();
-        int hp[SAMP_LISTS_PER_LANE];
-        uint32_t hk[SAMP_LISTS_PER_LANE];
-        int hi[SAMP_LISTS_PER_LANE];
-#pragma unroll
-        for (int j = 0; j < SAMP_LISTS_PER_LANE; j++) {
-            const int c = lane + 64 * j;
-            hp[j] = 0;
-            hk[j] = c < n_chunks ? s_key[c * k] : 0u;
-            hi[j] = c < n_chunks ? s_id[c * k] : INT_MAX;
+    // repeat penalty (sampler.c:47-55): each occurrence of an id in
+    // last_tokens applies the rule to the current value, in turn
+    if (P.repeat_penalty != 1.0f && t < P.n_uniq) {
+        const int id = P.uniq[t];
+        if (id >= base && id < base + SAMP_CHUNK && id < n) {
+            float v = s_v[id - base];
+            for (int j = 0; j < P.count[t]; j++) v = v < 0.0f ? v * P.repeat_penalty : v / P.repeat_penalty;
+            s_v[id - base] = v;
         }
-        for (int p = 0; p < k; p++) {
-            // this lane's best head: the larger key, then the lower index
-            const bool second = hk[1] > hk[0] || (hk[1] == hk[0] && hi[1] < hi[0]);
-            const uint32_t bk = second ? hk[1] : hk[0];
-            const int bi = second ? hi[1] : hi[0];
-            uint32_t m;
-            const bool me = samp_pick(bk, bi, m);
-            if (me) {
-                s_oid[p] = bi;
-                s_oval[p] = samp_val(bk);
-                const int c = lane + (second ? 64 : 0);
-                const int np = (second ? hp[1] : hp[0]) + 1;
-                const uint32_t nk = np < k ? s_key[c * k + np] : 0u;
-                const int ni = np < k ? s_id[c * k + np] : INT_MAX;
-                if (second) {
-                    hp[1] = np;
-                    hk[1] = nk;
-                    hi[1] = ni;
-                } else {
-                    hp[0] = np;
-                    hk[0] = nk;
-                    hi[0] = ni;
-                }
+    }
+    __syncthreads();
+    uint64_t c[SAMP_PER_THREAD];
+#pragma unroll
+    for (int m = 0; m < SAMP_PER_THREAD; m++) {
+        const int i = t + 256 * m;               // element i of the chunk
+        float v = s_v[i];
+        if (P.temp > 0.0f) v = v / P.temp;        // sampler.c:56-58
+        c[m] = base + i < n ? samp_comp(samp_key(v), base + i) : 0ull;
+    }
+    const int valid = n - base < SAMP_CHUNK ? n - base : SAMP_CHUNK;
+    const int kk = k < valid ? k : valid;
+    bool sel[SAMP_PER_THREAD];
+    wg_topk<SAMP_PER_THREAD>(c, kk, sel, s_hist, s_info, s_m);
+    int cnt = 0;
+#pragma unroll
+    for (int m = 0; m < SAMP_PER_THREAD; m++) cnt += sel[m];
+    int total;
+    int pos = wg_excl_scan(cnt, s_w, &total);
+    // The candidates go out with device-scope stores (coherent across the
+    // XCDs' L2s without a cache write-back), each wave waits for its stores
+    // to complete, then one increment of the counter per workgroup: the
+    // workgroup that brings it to n_chunks saw every other one's stores done
+    // and merges.  No cache-wide fence is needed.
+    uint64_t *mine = cand + (size_t)blockIdx.x * k;
+#pragma unroll
+    for (int m = 0; m < SAMP_PER_THREAD; m++)
+        if (sel[m]) __hip_atomic_store(mine + pos++, c[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = kk + t; i < k; i += 256) __hip_atomic_store(mine + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0)
+        s_last = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(n_chunks - 1);
+    __syncthreads();
+    if (!s_last) return;
+    uint64_t g[SAMP_MERGE_PER_THREAD];
+    const int total_c = n_chunks * k;
+#pragma unroll
+    for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++) {
+        const int i = t + 256 * j;
+        g[j] = i < total_c ? __hip_atomic_load(cand + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+    }
+    bool gs[SAMP_MERGE_PER_THREAD];
+    wg_topk<SAMP_MERGE_PER_THREAD>(g, k, gs, s_hist, s_info, s_m);
+    cnt = 0;
+#pragma unroll
+    for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++) cnt += gs[j];
+    pos = wg_excl_scan(cnt, s_w, &total);
+#pragma unroll
+    for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++)
+        if (gs[j]) s_win[pos++] = g[j];
+    __syncthreads();
+    if (t < 64) {
+        const int lane = t;
+        uint64_t v = lane < k ? s_win[lane] : 0ull;
+        // bitonic sort, descending over the 64 lanes
+#pragma unroll
+        for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const uint64_t o = shfl_xor64(v, stride);
+                const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
+                v = keep_max ? (v > o ? v : o) : (v < o ? v : o);
+            }
+        const int id = (int)~(uint32_t)v;
+        const float val = samp_val((uint32_t)(v >> 32));
+        // results to pinned host memory with system-scope stores, waited for
+        // before the completion marker is stored
+        auto put = [&](int i, int v) { __hip_atomic_store(out + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };
+        if (lane < k) {
+            put(lane, id);
+            put(64 + lane, __float_as_int(val));
+        }
+        if (sample) {
+            int drew = 0;
+            uint64_t sd = seed;
+            const int tok = samp_pick_wave(val, id, k, P.temp, top_p, sd, &drew);
+            if (lane == 0) {
+                put(128, tok);
+                put(129, drew);
+                put(130, (int)(uint32_t)sd);
+                put(131, (int)(uint32_t)(sd >> 32));
             }
         }
-    }
-    __syncthreads();
-    const int t = (int)threadIdx.x;
-    if (t < k) {
-        ids[t] = s_oid[t];
-        vals[t] = s_oval[t];
-    }
-    if (sample && t == 0) {
-        int drew = 0;
-        uint64_t sd = seed;
-        res[0] = samp_pick_token(s_oid, s_oval, k, temp, top_p, sd, &drew);
-        res[1] = drew;
-        res[2] = (int)(uint32_t)sd;
-        res[3] = (int)(uint32_t)(sd >> 32);
+        if (lane == 0) __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // for the next call
+        __builtin_amdgcn_s_waitcnt(0);
+        if (lane == 0) put(132, seq);
     }
 }
 
 // ------------------------------------------------------------------ host --
+static int *g_samp_host = nullptr;      // pinned: the kernel's results
+static int g_samp_seq = 0;
+
+// Wait for the kernel's completion marker in pinned memory: a host spin on
+// one word is far quicker than a stream synchronisation.  Every few
+// thousand polls the stream is queried, so a launch that failed, or a
+// kernel that finished without the marker reaching the host, ends the wait.
+static int wait_marker(hipStream_t st, int seq)
+{
+    volatile int *m = g_samp_host + 132;
+    for (long i = 1;; i++) {
+        if (*m == seq) return QMAG_OK;
+        if (i % 4096 == 0) {
+            const hipError_t e = hipStreamQuery(st);
+            if (e == hipSuccess) {
+                if (*m == seq) return QMAG_OK;
+                return fail(QMAG_ERR_KERNEL, "sampler: kernel finished without its completion marker");
+            }
+            if (e != hipErrorNotReady) return hip_fail(e, "sampler wait", __FILE__, __LINE__);
+        }
+    }
+}
+
 static int sample_run(int n_vocab, const float *logits, const qmag_sampler *s, int max_k, bool sample, float top_p,
                       int *ids, float *vals, int res[4])
 {
@@ -361,11 +429,20 @@ static int sample_run(int n_vocab, const float *logits, const qmag_sampler *s, i
     SampParams P;
     P.temp = s->temp;
     P.repeat_penalty = s->repeat_penalty;
-    P.n_last = s->n_last < 0 ? 0 : s->n_last > 64 ? 64 : s->n_last;
-    for (int i = 0; i < 64; i++) P.last[i] = i < P.n_last ? s->last_tokens[i] : -1;
+    const int n_last = s->n_last < 0 ? 0 : s->n_last > 64 ? 64 : s->n_last;
+    P.n_uniq = 0;
+    for (int i = 0; i < n_last; i++) {
+        const int id = s->last_tokens[i];
+        if (id < 0 || id >= n_vocab) continue;             // sampler.c:50
+        int u = 0;
+        while (u < P.n_uniq && P.uniq[u] != id) u++;
+        if (u == P.n_uniq) {
+            P.uniq[P.n_uniq] = id;
+            P.count[P.n_uniq++] = 0;
+        }
+        P.count[u]++;
+    }
     const int n_chunks = (n_vocab + SAMP_CHUNK - 1) / SAMP_CHUNK;
-    const size_t cand = (size_t)n_chunks * k;
-    const size_t need = cand * 8 + 256 + SAMP_MAX_K * 8 + 64;
     hipStream_t st = ctx().stream;
     // logits computed from persistent-decode outputs: have any expired wait
     // of those launches recovered first (qmag_d2h does the same)
@@ -373,24 +450,31 @@ static int sample_run(int n_vocab, const float *logits, const qmag_sampler *s, i
         const int fst = fused_status();
         if (fst) return fst;
     }
+    const size_t cand_bytes = sizeof(uint64_t) * (size_t)SAMP_MAX_CHUNKS * SAMP_MAX_K;
     int wst = QMAG_OK;
-    uint8_t *ws = (uint8_t *)workspace(WS_SAMP, need, &wst);
+    uint8_t *ws = (uint8_t *)workspace(WS_SAMP, cand_bytes + 256, &wst);
     if (!ws) return wst;
-    uint32_t *ckey = (uint32_t *)ws;
-    int *cid = (int *)(ws + cand * 4);
-    int *d_ids = (int *)(ws + ((cand * 8 + 255) & ~(size_t)255));
-    float *d_vals = (float *)(d_ids + SAMP_MAX_K);
-    int *d_res = (int *)(d_vals + SAMP_MAX_K);
-    const size_t lds = cand * 8;                       // <= 127 chunks * 64 * 8 bytes
-    hipLaunchKernelGGL(cand_chunk_kernel, dim3(n_chunks), dim3(256), 0, st, logits, n_vocab, P, k, ckey, cid);
+    unsigned *done = (unsigned *)(ws + cand_bytes);
+    static uint8_t *counted = nullptr;
+    if (ws != counted) {
+        // a new buffer: the completion counter starts at zero; each
+        // launch's last workgroup puts it back
+        QMAG_HIP(hipMemsetAsync(done, 0, sizeof(unsigned), st));
+        counted = ws;
+    }
+    if (!g_samp_host) {
+        QMAG_HIP(hipHostMalloc((void **)&g_samp_host, 136 * sizeof(int), hipHostMallocDefault));
+        g_samp_host[132] = 0;
+    }
+    const int seq = ++g_samp_seq == 0 ? ++g_samp_seq : g_samp_seq;    // never 0, the initial marker
+    hipLaunchKernelGGL(sampler_kernel, dim3(n_chunks), dim3(256), 0, st, logits, n_vocab, P, k, n_chunks,
+                       (uint64_t *)ws, done, sample ? 1 : 0, s->seed, top_p, g_samp_host, seq);
     QMAG_HIP(hipGetLastError());
-    hipLaunchKernelGGL(cand_merge_kernel, dim3(1), dim3(256), lds, st, ckey, cid, n_chunks, k, d_ids, d_vals,
-                       sample ? 1 : 0, s->seed, s->temp, top_p, d_res);
-    QMAG_HIP(hipGetLastError());
-    if (ids) QMAG_HIP(hipMemcpyAsync(ids, d_ids, sizeof(int) * k, hipMemcpyDeviceToHost, st));
-    if (vals) QMAG_HIP(hipMemcpyAsync(vals, d_vals, sizeof(float) * k, hipMemcpyDeviceToHost, st));
-    if (sample) QMAG_HIP(hipMemcpyAsync(res, d_res, sizeof(int) * 4, hipMemcpyDeviceToHost, st));
-    QMAG_HIP(hipStreamSynchronize(st));
+    const int wst2 = wait_marker(st, seq);
+    if (wst2) return wst2;
+    if (ids) memcpy(ids, g_samp_host, sizeof(int) * k);
+    if (vals) memcpy(vals, g_samp_host + 64, sizeof(float) * k);
+    if (sample) memcpy(res, g_samp_host + 128, sizeof(int) * 4);
     return k;
 }
 

@@ -73,7 +73,7 @@ def test_candidates_vs_oracle(qm, orc, temp, top_k, max_k, rp):
     assert gi.size == min(max(top_k, 1), max_k)
 
 
-@pytest.mark.parametrize("n", [1, 3, 63, 64, 1000, 1024, 4095, 4097, 8191, 127 * 4096])
+@pytest.mark.parametrize("n", [1, 3, 63, 64, 1000, 1024, 4095, 4097, 8191, 128 * 4096])
 def test_candidates_vocab_edges(qm, orc, n):
     """Ragged vocabularies: k clamps to n_vocab (sampler.c:63-66), the last
     chunk is partial, the largest vocabulary the device merge takes."""
@@ -96,8 +96,8 @@ def test_candidates_ties(qm, orc):
 
 def test_candidates_rejects(qm):
     s = qm.Sampler.init(top_k=40)
-    d = qm.DBuf.from_array(np.zeros(127 * 4096 + 1, np.float32))
-    for n, mk in ((127 * 4096 + 1, 40), (1000, 0), (1000, 65), (0, 40)):
+    d = qm.DBuf.from_array(np.zeros(128 * 4096 + 1, np.float32))
+    for n, mk in ((128 * 4096 + 1, 40), (1000, 0), (1000, 65), (0, 40)):
         with pytest.raises(qm.QmagError, match="sampler"):
             qm.sampler_candidates_dev(d.ptr, n, s, mk)
 
