@@ -247,7 +247,7 @@ def aux_sampler(seconds: float, cpu_seconds: float) -> dict:
     gpu_us = (time.perf_counter() - t0) / n * 1e6
     res = {"config": "sampler: 151,936 logits, top_k 20 (max 40), temp 1, top_p 0.95, repeat penalty 1.1",
            "gpu_us_per_token": gpu_us, "gpu_calls": n,
-           "note": "host wall time per call including the launch of both kernels and the 16-byte readback"}
+           "note": "host wall time per call: the launch, the kernel and the wait for its result in pinned host memory"}
     if cpu_seconds > 0:
         orc = _orc()
         lh = logits.download(np.float32)
