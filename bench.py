@@ -43,8 +43,9 @@ METRIC = "MoE FFN decode tokens/s + achieved HBM GB/s (% of peak), Q4_K/Q6_K, 1 
 # HBM bytes per launch of the fused decode kernel as built from this tree,
 # from two rocprofv3 counter passes over bench.py (FETCH_SIZE x 2.000 +
 # WRITE_SIZE x 1.000, the factors read off a 1 GiB copy kernel in the same
-# runs); re-measured whenever the kernel changes.
-FUSED_TRAFFIC_BYTES = 869.6e6
+# runs, profiles/moe_decode_kernel_c4_hbm_counters.md); re-measured whenever
+# the kernel changes.
+FUSED_TRAFFIC_BYTES = 869.8e6
 
 
 def log(msg: str) -> None:
