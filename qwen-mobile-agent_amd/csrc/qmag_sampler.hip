@@ -28,6 +28,8 @@
 #include <limits.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "qmag_internal.h"
 
 namespace qmag {
@@ -395,6 +397,9 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
 // ------------------------------------------------------------------ host --
 static int *g_samp_host = nullptr;      // pinned: the kernel's results
 static int g_samp_seq = 0;
+// one sampling call at a time per process: the pinned results, the marker
+// sequence and the workspace are shared
+static std::mutex g_samp_mu;
 
 // Wait for the kernel's completion marker in pinned memory: a host spin on
 // one word is far quicker than a stream synchronisation.  Every few
@@ -444,6 +449,7 @@ static int sample_run(int n_vocab, const float *logits, const qmag_sampler *s, i
     }
     const int n_chunks = (n_vocab + SAMP_CHUNK - 1) / SAMP_CHUNK;
     hipStream_t st = ctx().stream;
+    std::lock_guard<std::mutex> guard(g_samp_mu);
     // logits computed from persistent-decode outputs: have any expired wait
     // of those launches recovered first (qmag_d2h does the same)
     if (fused_pending()) {
