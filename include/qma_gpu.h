@@ -123,7 +123,8 @@ int qmag_prof_read(int kernel_id, long *count, double *total_ms);
    per-stage launch sequence (same results within the fp32 tolerance). */
 #define QMAG_OPT_FUSED 1
 /* QMAG_OPT_TRACE (default 0): the fused decode kernel records, per
-   workgroup and layer, up to 8 phase timestamps of the 100 MHz device
+   workgroup and layer (the first 64 layers of a launch), up to 8 phase
+   timestamps of the 100 MHz device
    real-time counter (slot 0 is the layer start; the other slots mark the
    phases of the workgroup's role, 0 where it has none); qmag_trace_read
    copies the last launch's [512][n_layer][8] uint64 array to the host. */

@@ -67,6 +67,7 @@ constexpr int CORE = 128;                         // core workgroups
 constexpr int CROWS = N / CORE;                   // 16 hidden rows per core workgroup
 constexpr int WROWS = CROWS / 4;                  // 4 per core wave
 constexpr int NLOG = 256 / CORE;                  // 2 router logits per core workgroup
+constexpr int TR_LAYERS = 64;                     // layers a traced launch records
 constexpr int GU_WAVES = WGS * 4;                 // every wave takes routed gate/up row pairs
 constexpr int MAX_RP = (8 * F + GU_WAVES - 1) / GU_WAVES;      // 2 routed row pairs per wave
 // the shared expert's row pair i: workgroup SH_WG0 + i/2, wave 2 + i%2 (the
@@ -458,6 +459,7 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
     __shared__ int s_sel[8];
     __shared__ float s_w[8];
     __shared__ int s_vote[4][4];
+    __shared__ uint32_t s_tr[TR_LAYERS][8];        // traced launches: phase stamps until the end
 
     const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), tid = (int)threadIdx.x;
     const int b = (int)blockIdx.x;
@@ -468,6 +470,9 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
     // set by an earlier launch whose wait expired: this launch exits at its
     // first barrier, before any output is written (read now, used there)
     const bool pre_abort = ld_flag(abort_flag) != 0;
+    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+    if (trace && threadIdx.x == 0)
+        for (int i = 0; i < TR_LAYERS * 8; i++) s_tr[i / 8][i % 8] = 0;
     // the 256 logits of replica rep, lane's pairs l and l + 64 (experts
     // l + 64j, j = 0..3); a half is needed only for an expert below E
     auto logit_pairs = [&](int E) {
@@ -506,9 +511,13 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
     const int dq = lane & 7, dg = lane >> 3;
 
     // optional phase timestamps (100 MHz real-time counter), thread 0 only
+    // They collect in LDS (32-bit offsets from the workgroup's start, the
+    // first TR_LAYERS layers) and go to memory once, when the workgroup
+    // ends: a store to memory inside the layers would sit in the wave's
+    // memory counter, which every later wait for a load also waits on.
 #define TR(i)                                                                              \
-    if (trace && threadIdx.x == 0)                                                         \
-        trace[((size_t)b * n_layer + l) * 8 + (i)] = __builtin_amdgcn_s_memrealtime();
+    if (trace && threadIdx.x == 0 && l < TR_LAYERS)                                        \
+        s_tr[l][i] = (uint32_t)(__builtin_amdgcn_s_memrealtime() - t_start) | 0x80000000u;
 
     // core: rows r0 .. r0+15; wave wv owns r0+4wv .. +3, lane i < 4 keeps the
     // residual value of row r0 + 4wv + i
@@ -857,6 +866,14 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
             // LDS is rewritten next layer only after this barrier
             __syncthreads();
         }
+    }
+    if (trace && threadIdx.x == 0) {
+        const int nl = n_layer < TR_LAYERS ? n_layer : TR_LAYERS;
+        for (int l = 0; l < nl; l++)
+            for (int i = 0; i < 8; i++) {
+                const uint32_t v = s_tr[l][i];        // set stamps have the top bit
+                if (v) trace[((size_t)b * n_layer + l) * 8 + i] = t_start + (v & 0x7fffffffu);
+            }
     }
 #undef TR
 }

@@ -205,3 +205,47 @@ def test_paged_layer_rejects_small_records(qm, orc, small):
         c.close()
         qm.Gguf.free_moe_layer(L)
         g.close()
+
+
+def test_concurrent_gets_of_hinted_records(qm, orc, small):
+    """The reference calls qma_ecache_get from its pool workers at once
+    (nn.c:677-678); records a hint named are pinned for the generation, so
+    their addresses stay valid while other threads get.  Four host threads
+    get the hinted records of a layer concurrently (reader threads on) and
+    every address holds the file's bytes."""
+    import threading
+    g = qm.Gguf(str(small))
+    rec = g.expert_record_bytes()
+    recs = _records(g, 2)
+    c = qm.ECache(40 * rec, rec, fetch=qm.gguf_fetch_fn(), user=g.h)
+    c.io_start(4, 4)
+    errors = []
+    try:
+        for layer in range(2):
+            ids = list(range(3 + layer, 3 + layer + 10))          # 10 = 40 slots / 4
+            c.hint(layer, ids)
+            got = {}
+
+            def worker(tid):
+                try:
+                    for e in ids[tid::4] + ids[::-1][tid::4]:
+                        p = c.get(layer, e)
+                        if not p:
+                            errors.append(("null", layer, e))
+                        got.setdefault(e, set()).add(p)
+                except Exception as exc:                     # surfaced below
+                    errors.append(exc)
+
+            th = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+            for t in th:
+                t.start()
+            for t in th:
+                t.join()
+            assert not errors, errors
+            c.drain()
+            for e, ps in got.items():
+                assert len(ps) == 1, (layer, e, ps)                # one slot per record
+                _check_bytes(qm, recs, (layer, e), next(iter(ps)), rec)
+    finally:
+        c.close()
+        g.close()
