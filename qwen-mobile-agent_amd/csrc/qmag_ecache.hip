@@ -24,7 +24,9 @@
 #include <condition_variable>
 #include <deque>
 #include <mutex>
+#include <set>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "qmag_internal.h"
@@ -55,6 +57,11 @@ int32_t key_of(int layer, int expert) { return (int32_t)(((uint32_t)layer << 16)
 struct qmag_ecache {
     std::vector<Slot> slot;
     int n_slots = 0;
+    // the resident keys (key -> slot) and the empty slots in index order, so
+    // that neither a lookup nor the first-empty-slot rule scans every slot
+    // (an HBM budget holds over 100,000 records of 2 MB)
+    std::unordered_map<int32_t, int> index;
+    std::set<int> empty;
     size_t rec_bytes = 0, slot_bytes = 0;
     uint64_t clock = 0, hits = 0, misses = 0, bytes_read = 0, evictions = 0, prefetched = 0, spec_issued = 0;
     uint32_t rng = 0x9e3779b9u;
@@ -91,9 +98,8 @@ using qmag::fail;
 
 int lookup(const qmag_ecache *c, int32_t key)
 {
-    for (int i = 0; i < c->n_slots; i++)
-        if (c->slot[i].key == key) return i;
-    return -1;
+    const auto it = c->index.find(key);
+    return it == c->index.end() ? -1 : it->second;
 }
 
 bool is_held(const qmag_ecache *c, int i)
@@ -114,8 +120,7 @@ bool pinned(const qmag_ecache *c, int i)
 // hits, then least recent; LRU: least recent); else the first unpinned
 int victim(qmag_ecache *c)
 {
-    for (int i = 0; i < c->n_slots; i++)
-        if (c->slot[i].state == EC_EMPTY) return i;
+    if (!c->empty.empty()) return *c->empty.begin();     // the lowest empty slot
     int best = -1;
     uint32_t bh = 0;
     uint64_t bl = 0;
@@ -140,7 +145,12 @@ int victim(qmag_ecache *c)
 
 void take(qmag_ecache *c, int vi, int32_t key)
 {
-    if (c->slot[vi].key >= 0) c->evictions++;
+    if (c->slot[vi].key >= 0) {
+        c->evictions++;
+        c->index.erase(c->slot[vi].key);
+    }
+    c->empty.erase(vi);
+    c->index[key] = vi;
     c->slot[vi].key = key;
     c->slot[vi].state = EC_INFLIGHT;
 }
@@ -175,6 +185,8 @@ void claim(qmag_ecache *c, int vi, int32_t key, bool fresh)
 void drop(qmag_ecache *c, int vi)
 {
     Slot &s = c->slot[vi];
+    if (s.key >= 0) c->index.erase(s.key);
+    c->empty.insert(vi);
     s.key = -1;
     s.state = EC_EMPTY;
     s.fresh = 0;
@@ -368,6 +380,7 @@ int qmag_ecache_init(qmag_ecache **out, size_t budget_bytes, size_t rec_bytes, i
         if (c->n_slots < 4) c->n_slots = 4;
     }
     c->slot.assign((size_t)c->n_slots, Slot{});
+    for (int i = 0; i < c->n_slots; i++) c->empty.insert(c->empty.end(), i);
     c->slot_bytes = (rec_bytes + SLOT_ALIGN - 1) / SLOT_ALIGN * SLOT_ALIGN;
     hipError_t e = hipSuccess;
     if (c->n_slots > 0) {
@@ -403,8 +416,21 @@ void qmag_ecache_free(qmag_ecache *c)
 
 void qmag_ecache_clear(qmag_ecache *c)
 {
+    // ecache.c:522-540, after the reads already queued or in flight have
+    // landed: a reader still holding a job would otherwise copy its record
+    // into a slot that may since hold another key
     if (!c) return;
-    std::lock_guard<std::mutex> g(c->mu);
+    std::unique_lock<std::mutex> lk(c->mu);
+    mark_use(c);
+    c->done.wait(lk, [&] {
+        if (!c->q.empty()) return false;
+        for (const Slot &s : c->slot)
+            if (s.state == EC_INFLIGHT) return false;
+        return true;
+    });
+    c->index.clear();
+    c->empty.clear();
+    for (int i = 0; i < c->n_slots; i++) c->empty.insert(c->empty.end(), i);
     for (Slot &s : c->slot) {
         s.key = -1;
         s.state = EC_EMPTY;

@@ -89,6 +89,9 @@ def test_policy_matches_oracle(qm, orc, small, n_slots, policy, nthreads):
             elif r < 0.25:
                 c.release()
                 m.release()
+            elif r < 0.255:
+                c.clear()                                  # everything evicted, counters zeroed
+                m.clear()
             else:
                 hold = r < 0.35
                 p = c.hold(layer, e) if hold else c.get(layer, e)
