@@ -287,7 +287,9 @@ int qmag_gguf_free_moe_layer(qmag_moe_layer *L);
    qmag_gguf *): the record of (layer, expert) copied from the mapping, as
    expert_fetch (nn.c:1564-1595) preads it; -1 when the layer or expert does
    not exist.  qmag_gguf_expert_record_bytes gives the largest layer's record
-   size (down types vary per layer, nn.c:1601-1605). */
+   size (down types vary per layer, nn.c:1601-1605); a cache given this
+   callback must have records at least that large, and refuses it otherwise
+   (io_start returns QMAG_ERR_ARG, a get that would read returns NULL). */
 int qmag_gguf_fetch_expert(void *user, int layer, int expert, uint8_t *dst);
 int qmag_gguf_expert_record_bytes(const qmag_gguf *g, size_t *rec);
 

@@ -89,6 +89,7 @@ struct qmag_ecache {
     std::vector<hipEvent_t> th_ev;
     qmag_fetch_fn fetch = nullptr;
     void *fetch_user = nullptr;
+    const void *fits_user = nullptr;         // a GGUF file whose records fit rec_bytes
     int hip_error = 0;                       // first HIP failure seen by a reader
 };
 
@@ -276,6 +277,23 @@ void reader(qmag_ecache *c, int t)
     }
 }
 
+// The fetch callback fills rec_bytes of staging and cannot be told the size.
+// The library's own GGUF callback writes the record of the layer asked for,
+// and down types vary per layer: check once per file that its largest
+// record fits (under the lock).
+bool fetch_fits(qmag_ecache *c, qmag_fetch_fn fetch, void *user)
+{
+    if (fetch != qmag_gguf_fetch_expert || !user || user == c->fits_user) return true;
+    size_t rec = 0;
+    if (qmag_gguf_expert_record_bytes((const qmag_gguf *)user, &rec) != QMAG_OK) return false;
+    if (rec > c->rec_bytes) {
+        fail(QMAG_ERR_ARG, "ecache: records of %zu bytes, the file's largest has %zu", c->rec_bytes, rec);
+        return false;
+    }
+    c->fits_user = user;
+    return true;
+}
+
 // the calling-thread part of every public call: order later copies behind
 // the library-stream work queued so far
 void mark_use(qmag_ecache *c)
@@ -317,6 +335,7 @@ const uint8_t *get_locked(qmag_ecache *c, std::unique_lock<std::mutex> &lk, int 
         return nullptr;
     }
     // not resident, not hinted: read it here, through a slot
+    if (!fetch_fits(c, fetch, user)) return nullptr;
     const int vi = victim(c);
     if (vi < 0) return nullptr;
     claim(c, vi, key, false);
@@ -456,6 +475,10 @@ int qmag_ecache_io_start(qmag_ecache *c, qmag_fetch_fn fetch, void *user, int nt
     if (depth < 1) depth = 1;
     if (depth > c->n_slots / 4) depth = c->n_slots / 4;
     if (depth < 1) return QMAG_OK;
+    {
+        std::lock_guard<std::mutex> g(c->mu);
+        if (!fetch_fits(c, fetch, user)) return QMAG_ERR_ARG;
+    }
     for (int t = 0; t < nthreads; t++) {
         uint8_t *p = nullptr;
         hipEvent_t ev = nullptr;

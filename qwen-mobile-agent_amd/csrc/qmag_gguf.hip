@@ -245,7 +245,14 @@ int qmag_gguf_open(const char *path, qmag_gguf **out)
         }
         if (t.ne[0] % (int64_t)blk != 0)
             return fail_open(err(QMAG_ERR_ARG, "gguf: tensor %s: ne0 not block multiple", t.name.c_str()));
-        t.nbytes = (size_t)(t.ne[0] / (int64_t)blk) * bs * (size_t)t.ne[1] * (size_t)t.ne[2];
+        // (each dimension is below 2^40, so the product can overflow: a
+        // wrapped size would pass the range check below with shapes that
+        // name more bytes than are uploaded)
+        size_t nb = 0;
+        if (__builtin_mul_overflow((size_t)(t.ne[0] / (int64_t)blk), bs, &nb) ||
+            __builtin_mul_overflow(nb, (size_t)t.ne[1], &nb) || __builtin_mul_overflow(nb, (size_t)t.ne[2], &nb))
+            return fail_open(err(QMAG_ERR_ARG, "gguf: tensor %s is too large", t.name.c_str()));
+        t.nbytes = nb;
         if (t.off > data_size || t.nbytes > data_size - t.off)
             return fail_open(err(QMAG_ERR_ARG, "gguf: tensor %s out of file range", t.name.c_str()));
         if (!g->by_name.emplace(t.name, i).second)

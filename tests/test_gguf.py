@@ -93,6 +93,9 @@ def test_rejects_malformed_files(qmlib, orc, tmp_path):
     gw.write_gguf(bad, [], [("d.weight", gw.T_F32, [4], np.zeros(4, np.float32)),
                             ("d.weight", gw.T_F32, [4], np.zeros(4, np.float32))])
     _expect_open_error(qmlib, bad, "duplicate tensor")
+    # dimensions whose byte count wraps 64 bits (2^32 blocks * 144 B * 2^40 * 2^40 = 0 mod 2^64)
+    gw.write_gguf(bad, [], [("w.weight", gw.T_Q4_K, [1 << 40, 1 << 40, 1 << 40], np.zeros(144, np.uint8))])
+    _expect_open_error(qmlib, bad, "too large")
     # an array of strings whose declared count runs past the end of the file
     meta = struct.pack("<Q", 4) + b"toks" + struct.pack("<IIQ", gw.ARR, gw.STR, 1 << 40)
     bad.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + meta)

@@ -252,3 +252,32 @@ def test_concurrent_gets_of_hinted_records(qm, orc, small):
     finally:
         c.close()
         g.close()
+
+
+def test_gguf_fetch_needs_room_for_the_largest_record(qm, orc, tmp_path):
+    """The fetch callback cannot be told the staging size.  The file's layers
+    differ in down type (Q6_K, then Q4_K), so its records differ in size; a
+    cache sized for the smaller one refuses the GGUF callback instead of
+    letting it overrun the staging: no read starts, no slot is claimed."""
+    N, F, E, K = 256, 256, 8, 2
+    path = tmp_path / "mixed.gguf"
+    _write(orc, path, 2, N, F, E, K)
+    g = qm.Gguf(str(path))
+    big = g.expert_record_bytes()
+    small = big - (F * N // 256) * (210 - 144)          # a Q4_K-down layer's record
+    c = qm.ECache(8 * small, small, fetch=qm.gguf_fetch_fn(), user=g.h)
+    try:
+        assert c.get(1, 3) == 0 and c.get(0, 3) == 0
+        with pytest.raises(qm.QmagError, match="largest"):
+            c.io_start(2, 2)
+        st = c.stats()
+        assert st["misses"] == 0 and st["bytes_read"] == 0
+        assert all(c.slot_of(il, e) == -1 for il in range(2) for e in range(E))
+    finally:
+        c.close()
+    ok = qm.ECache(8 * big, big, fetch=qm.gguf_fetch_fn(), user=g.h)
+    try:
+        assert ok.get(1, 3) != 0 and ok.get(0, 3) != 0
+    finally:
+        ok.close()
+        g.close()
