@@ -405,15 +405,17 @@ static std::mutex g_samp_mu;
 // one word is far quicker than a stream synchronisation.  Every few
 // thousand polls the stream is queried, so a launch that failed, or a
 // kernel that finished without the marker reaching the host, ends the wait.
+// The marker is read with acquire ordering: the results, stored before it
+// by the kernel, are read after it.
 static int wait_marker(hipStream_t st, int seq)
 {
-    volatile int *m = g_samp_host + 132;
+    const int *m = g_samp_host + 132;
     for (long i = 1;; i++) {
-        if (*m == seq) return QMAG_OK;
+        if (__atomic_load_n(m, __ATOMIC_ACQUIRE) == seq) return QMAG_OK;
         if (i % 4096 == 0) {
             const hipError_t e = hipStreamQuery(st);
             if (e == hipSuccess) {
-                if (*m == seq) return QMAG_OK;
+                if (__atomic_load_n(m, __ATOMIC_ACQUIRE) == seq) return QMAG_OK;
                 return fail(QMAG_ERR_KERNEL, "sampler: kernel finished without its completion marker");
             }
             if (e != hipErrorNotReady) return hip_fail(e, "sampler wait", __FILE__, __LINE__);
