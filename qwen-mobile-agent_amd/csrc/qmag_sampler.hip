@@ -8,16 +8,17 @@
 // draw and the cumulative pick, and the pick's entry into last_tokens.
 //
 // One launch of one workgroup per 4096 logits.  Each workgroup applies the
-// penalty and the temperature to its logits and selects its k largest by a
-// radix select over unique 64-bit keys (the value's order-preserving bits,
-// then the complemented index, so equal values order by ascending index):
-// eight-bit digits, an LDS histogram per digit, stopping as soon as the
-// boundary digit's group is wholly in.  The last workgroup to finish (a
-// device-scope counter) selects the k largest of all chunks' candidates the
-// same way, sorts them with a 64-lane bitonic network, and, in the sampling
-// form, makes the pick with the reference's arithmetic, the candidates one
-// per lane and the sequential sums as uniform loops over the lanes.  Results
-// are written straight to pinned host memory.
+// penalty and the temperature to its logits and selects its k largest over
+// unique 64-bit keys (the value's order-preserving bits, then the
+// complemented index, so equal values order by ascending index): the k-th
+// largest of the threads' maxima bounds the answer from below, and the few
+// keys that reach it are sorted by one wave's bitonic network (an exact
+// radix select takes over when more than 128 reach it).  The last workgroup
+// to finish (a device-scope counter) selects the k largest of all chunks'
+// candidates the same way and, in the sampling form, makes the pick with the
+// reference's arithmetic, the candidates one per lane and the sequential
+// sums as uniform loops over the lanes.  Results are written straight to
+// pinned host memory.
 //
 // Among exactly equal values the lower index comes first.  The reference
 // keeps its candidates in a min-heap and sorts them with qsort, so which of
@@ -69,21 +70,55 @@ __device__ __forceinline__ uint64_t samp_comp(uint32_t key, int id)
     return ((uint64_t)key << 32) | (uint32_t)~(uint32_t)id;
 }
 
+// The value of lane (lane ^ m), m one of 1, 2, 4, 8, 16, 32 (a constant once
+// the callers' loops are unrolled), by DPP moves and the gfx950 lane swaps
+// instead of the LDS crossbar: xor 4 is a half-row mirror (xor 7) then a
+// quad reversal (xor 3), xor 8 a row mirror (xor 15) then a half-row mirror.
+constexpr int DPP_XOR3 = 0x1B;          // quad_perm [3,2,1,0]
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int m)
+{
+    const int x = (int)v;
+    switch (m) {
+    case 1: return (uint32_t)dpp_i<DPP_XOR1>(x);
+    case 2: return (uint32_t)dpp_i<DPP_XOR2>(x);
+    case 4: return (uint32_t)dpp_i<DPP_XOR3>(dpp_i<DPP_HALF_MIRROR>(x));
+    case 8: return (uint32_t)dpp_i<DPP_HALF_MIRROR>(dpp_i<DPP_MIRROR>(x));
+    case 16: {
+        // rows 1, 3 of the first result hold rows 0, 2; rows 0, 2 of the
+        // second hold rows 1, 3
+        auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane_id() & 16) ? p[0] : p[1];
+    }
+    default: {
+        auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane_id() & 32) ? p[0] : p[1];
+    }
+    }
+}
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m)
 {
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m);
+    const uint32_t lo = xor_lane((uint32_t)v, m), hi = xor_lane((uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+// a uniform lane's value
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int src)
+{
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), src);
     return ((uint64_t)hi << 32) | lo;
 }
 
-// inclusive prefix sum over the 64 lanes of a wave
+// inclusive prefix sum over the 64 lanes of a wave: a butterfly in which the
+// upper half of each block of 2d lanes adds the lower half's total
 __device__ __forceinline__ int wave_incl_scan(int v)
 {
     const int lane = lane_id();
+    int tot = v;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(v, d);
-        v += lane >= d ? o : 0;
+        const int o = (int)xor_lane((uint32_t)tot, d);
+        v += (lane & d) ? o : 0;
+        tot += o;
     }
     return v;
 }
@@ -126,7 +161,7 @@ __device__ void wg_select(const uint64_t (&c)[E], int need, bool (&sel)[E], uint
                            h3 = s_hist[4 * t + 3];
             const int local = (int)(h0 + h1 + h2 + h3);
             const int incl = wave_incl_scan(local);
-            const int tot = __shfl(incl, 63);
+            const int tot = __builtin_amdgcn_readlane(incl, 63);
             int above = tot - incl;                       // bins of the lanes above
             const uint32_t h[4] = {h0, h1, h2, h3};
 #pragma unroll
@@ -203,6 +238,109 @@ __device__ void wg_topk(uint64_t (&c)[E], int need, bool (&sel)[E], uint32_t *s_
     wg_select<E>(c, need, sel, s_hist, s_info);
 }
 
+// One compare-exchange step of a bitonic network over keys one per lane
+// (element index i): descending order overall.
+__device__ __forceinline__ uint64_t bitonic_step(uint64_t v, int i, int size, int stride)
+{
+    const uint64_t o = shfl_xor64(v, stride);
+    const bool keep_max = ((i & stride) == 0) == ((i & size) == 0);
+    return (v > o) == keep_max ? v : o;          // one compare: equal keys are equal values
+}
+
+// 64 keys, one per lane, sorted descending
+__device__ __forceinline__ uint64_t wave_sort64(uint64_t v)
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) v = bitonic_step(v, lane, size, stride);
+    return v;
+}
+
+// a bitonic sequence of 64 keys sorted descending (the merge half of the
+// network)
+__device__ __forceinline__ uint64_t wave_clean64(uint64_t v)
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int stride = 32; stride > 0; stride >>= 1) v = bitonic_step(v, lane, 64, stride);
+    return v;
+}
+
+// 128 keys (a: elements 0-63, b: 64-127, element 64r + lane) sorted
+// descending
+__device__ __forceinline__ void wave_sort128(uint64_t &a, uint64_t &b)
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= 128; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride == 64) {
+                const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+                a = hi;
+                b = lo;
+            } else {
+                a = bitonic_step(a, lane, size, stride);
+                b = bitonic_step(b, 64 + lane, size, stride);
+            }
+        }
+}
+
+// The `need` (<= 64) largest nonzero keys held across the workgroup (E per
+// thread, all distinct), sorted descending into s_out[0..need), by sorting
+// networks instead of radix passes: the need-th largest of the threads'
+// maxima bounds the answer from below (need threads hold a key at least
+// that large; it comes from the four waves' sorted maxima merged twice), and
+// when at most 128 keys reach the bound one wave sorts them.  Returns false
+// (nothing written, c untouched) when more reach it; the caller then takes
+// the radix select.  s_sort: 256 uint64, s_w: 4 ints, s_m: 4 uint64.
+template <int E>
+__device__ bool wg_topk_sorted(const uint64_t (&c)[E], int need, uint64_t *s_out, uint64_t *s_sort, int *s_w,
+                               uint64_t *s_m)
+{
+    const int t = (int)threadIdx.x, w = t >> 6, lane = t & 63;
+    uint64_t m = 0;
+#pragma unroll
+    for (int j = 0; j < E; j++) m = c[j] > m ? c[j] : m;
+    s_sort[t] = wave_sort64(m);
+    __syncthreads();
+    uint64_t v2 = 0;
+    if (w < 2) {                              // top 64 of waves (0, 1) and of (2, 3)
+        const uint64_t x = s_sort[128 * w + lane], y = s_sort[128 * w + 127 - lane];
+        v2 = wave_clean64(x > y ? x : y);
+    }
+    __syncthreads();                          // every read above is done
+    if (w < 2) s_sort[64 * w + lane] = v2;
+    __syncthreads();
+    if (w == 0) {                             // top 64 of all the maxima
+        const uint64_t x = s_sort[lane], y = s_sort[127 - lane];
+        const uint64_t v = wave_clean64(x > y ? x : y);
+        const uint64_t bound = readlane64(v, need - 1);
+        if (lane == 0) s_m[0] = bound;
+    }
+    __syncthreads();
+    const uint64_t bound = s_m[0];            // 0 when fewer than `need` threads hold keys
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < E; j++) cnt += c[j] && c[j] >= bound;
+    int total;
+    int pos = wg_excl_scan(cnt, s_w, &total);
+    if (total > 128) return false;            // workgroup-uniform
+#pragma unroll
+    for (int j = 0; j < E; j++)
+        if (c[j] && c[j] >= bound) s_sort[pos++] = c[j];
+    __syncthreads();
+    if (w == 0) {
+        uint64_t a = lane < total ? s_sort[lane] : 0ull, b = 64 + lane < total ? s_sort[64 + lane] : 0ull;
+        wave_sort128(a, b);
+        if (lane < need) s_out[lane] = a;
+    }
+    __syncthreads();
+    return true;
+}
+
 // the reference's xorshift64* (sampler.c:9-14)
 __device__ __forceinline__ uint64_t samp_rng(uint64_t &s)
 {
@@ -226,13 +364,13 @@ __device__ int samp_pick_wave(float lg, int id, int k, float temp, float top_p, 
     *drew = 0;
     const bool live = lane < k && lg > -1e29f;
     const unsigned long long lv = __ballot(live);
-    const int id0 = __shfl(id, 0);
+    const int id0 = __builtin_amdgcn_readlane(id, 0);
     if (!lv) return id0;                                   // all masked
     const int first_live = __ffsll(lv) - 1;
-    if (temp <= 0.0f) return __shfl(id, first_live);       // greedy: the best live one
+    if (temp <= 0.0f) return __builtin_amdgcn_readlane(id, first_live);   // greedy: the best live one
     float mx = live ? lg : -INFINITY;
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d));
+    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __uint_as_float(xor_lane(__float_as_uint(mx), d)));
     // expf correctly rounded, through double (the device's expf is not)
     const float e = live ? (float)exp((double)__fsub_rn(lg, mx)) : 0.0f;
     double z = 0.0;                                        // summed in index order
@@ -261,7 +399,7 @@ __device__ int samp_pick_wave(float lg, int id, int k, float temp, float top_p, 
         }
     }
     *drew = 1;
-    return __shfl(id, pick);
+    return __builtin_amdgcn_readlane(id, pick);
 }
 
 // out (pinned host memory): [0..63] ids, [64..127] values (float bits),
@@ -278,6 +416,7 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
     __shared__ uint64_t s_win[SAMP_MAX_K];
     __shared__ int s_last;
     __shared__ uint64_t s_m[4];
+    __shared__ uint64_t s_sort[256];
     float *s_v = (float *)s_v4;
     const int t = (int)threadIdx.x;
     const int base = (int)blockIdx.x * SAMP_CHUNK;
@@ -310,28 +449,34 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
     for (int m = 0; m < SAMP_PER_THREAD; m++) {
         const int i = t + 256 * m;               // element i of the chunk
         float v = s_v[i];
-        if (P.temp > 0.0f) v = v / P.temp;        // sampler.c:56-58
+        if (P.temp > 0.0f && P.temp != 1.0f) v = v / P.temp;     // sampler.c:56-58 (x / 1 = x)
         c[m] = base + i < n ? samp_comp(samp_key(v), base + i) : 0ull;
     }
     const int valid = n - base < SAMP_CHUNK ? n - base : SAMP_CHUNK;
     const int kk = k < valid ? k : valid;
-    bool sel[SAMP_PER_THREAD];
-    wg_topk<SAMP_PER_THREAD>(c, kk, sel, s_hist, s_info, s_m);
-    int cnt = 0;
-#pragma unroll
-    for (int m = 0; m < SAMP_PER_THREAD; m++) cnt += sel[m];
-    int total;
-    int pos = wg_excl_scan(cnt, s_w, &total);
     // The candidates go out with device-scope stores (coherent across the
     // XCDs' L2s without a cache write-back), each wave waits for its stores
     // to complete, then one increment of the counter per workgroup: the
     // workgroup that brings it to n_chunks saw every other one's stores done
     // and merges.  No cache-wide fence is needed.
     uint64_t *mine = cand + (size_t)blockIdx.x * k;
+    if (wg_topk_sorted<SAMP_PER_THREAD>(c, kk, s_win, s_sort, s_w, s_m)) {
+        for (int i = t; i < k; i += 256)
+            __hip_atomic_store(mine + i, i < kk ? s_win[i] : 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        bool sel[SAMP_PER_THREAD];
+        wg_topk<SAMP_PER_THREAD>(c, kk, sel, s_hist, s_info, s_m);
+        int cnt = 0;
 #pragma unroll
-    for (int m = 0; m < SAMP_PER_THREAD; m++)
-        if (sel[m]) __hip_atomic_store(mine + pos++, c[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int i = kk + t; i < k; i += 256) __hip_atomic_store(mine + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int m = 0; m < SAMP_PER_THREAD; m++) cnt += sel[m];
+        int total;
+        int pos = wg_excl_scan(cnt, s_w, &total);
+#pragma unroll
+        for (int m = 0; m < SAMP_PER_THREAD; m++)
+            if (sel[m]) __hip_atomic_store(mine + pos++, c[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int i = kk + t; i < k; i += 256)
+            __hip_atomic_store(mine + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (t == 0)
@@ -346,28 +491,25 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
         const int i = t + 256 * j;
         g[j] = i < total_c ? __hip_atomic_load(cand + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
     }
-    bool gs[SAMP_MERGE_PER_THREAD];
-    wg_topk<SAMP_MERGE_PER_THREAD>(g, k, gs, s_hist, s_info, s_m);
-    cnt = 0;
+    // the k largest of all chunks' candidates, sorted descending into s_win
+    const bool sorted = wg_topk_sorted<SAMP_MERGE_PER_THREAD>(g, k, s_win, s_sort, s_w, s_m);
+    if (!sorted) {
+        bool gs[SAMP_MERGE_PER_THREAD];
+        wg_topk<SAMP_MERGE_PER_THREAD>(g, k, gs, s_hist, s_info, s_m);
+        int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++) cnt += gs[j];
-    pos = wg_excl_scan(cnt, s_w, &total);
+        for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++) cnt += gs[j];
+        int total;
+        int pos = wg_excl_scan(cnt, s_w, &total);
 #pragma unroll
-    for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++)
-        if (gs[j]) s_win[pos++] = g[j];
-    __syncthreads();
+        for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++)
+            if (gs[j]) s_win[pos++] = g[j];
+        __syncthreads();
+    }
     if (t < 64) {
         const int lane = t;
         uint64_t v = lane < k ? s_win[lane] : 0ull;
-        // bitonic sort, descending over the 64 lanes
-#pragma unroll
-        for (int size = 2; size <= 64; size <<= 1)
-#pragma unroll
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                const uint64_t o = shfl_xor64(v, stride);
-                const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
-                v = keep_max ? (v > o ? v : o) : (v < o ? v : o);
-            }
+        if (!sorted) v = wave_sort64(v);
         const int id = (int)~(uint32_t)v;
         const float val = samp_val((uint32_t)(v >> 32));
         // results to pinned host memory with system-scope stores, waited for
