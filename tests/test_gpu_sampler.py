@@ -94,6 +94,20 @@ def test_candidates_ties(qm, orc):
     assert list(gi[gv == boundary]) == list(np.flatnonzero(logits == boundary)[:np.count_nonzero(gv == boundary)])
 
 
+def test_candidates_concentrated_chunk(qm, orc):
+    """The large logits all on 16 threads of one chunk (ids t + 256m, t < 16):
+    the k-th largest of the threads' maxima then lies among the small values,
+    more than 128 keys reach that bound, and the exact radix selection takes
+    over -- in the chunk and in the merge."""
+    rng = np.random.default_rng(11)
+    logits = rng.standard_normal(V).astype(np.float32)
+    ids = (np.arange(16)[:, None] + 256 * np.arange(16)[None, :]).ravel() + 4096 * 7
+    logits[ids] = (5.0 + rng.standard_normal(ids.size)).astype(np.float32)
+    for top_k in (64, 40, 8):
+        gi, _ = _check_candidates(qm, orc, logits, dict(temp=1.0, top_k=top_k, repeat_penalty=1.0), 64)
+        assert set(gi.tolist()) <= set(ids.tolist())
+
+
 def test_candidates_rejects(qm):
     s = qm.Sampler.init(top_k=40)
     d = qm.DBuf.from_array(np.zeros(128 * 4096 + 1, np.float32))
