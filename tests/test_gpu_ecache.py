@@ -281,3 +281,42 @@ def test_gguf_fetch_needs_room_for_the_largest_record(qm, orc, tmp_path):
     finally:
         ok.close()
         g.close()
+
+
+def test_clear_waits_for_reads_in_flight(qm, orc, small):
+    """clear() while reader threads still fetch hinted records (a slow
+    callback): it returns only once they have landed, leaves every slot
+    empty and the counters zero, and later reads put the right bytes in the
+    slots they claim."""
+    import time
+    g = qm.Gguf(str(small))
+    rec = g.expert_record_bytes()
+    recs = _records(g, 2)
+    started = []
+
+    def slow_fetch(user, layer, expert, dst):
+        started.append((layer, expert))
+        time.sleep(0.02)
+        b = recs.get((layer, expert))
+        if b is None:
+            return -1
+        C.memmove(dst, b.ctypes.data, b.size)
+        return 0
+
+    c = qm.ECache(40 * rec, rec, fetch=slow_fetch)
+    try:
+        c.io_start(4, 8)
+        c.hint(0, list(range(10)))                       # 8 reads start at once
+        c.prefetch(1, [20, 21, 22])
+        c.clear()
+        assert len(started) >= 8
+        st = c.stats()
+        assert (st["hits"], st["misses"], st["bytes_read"], st["prefetched"], st["spec_issued"]) == (0, 0, 0, 0, 0)
+        assert all(c.slot_of(il, e) == -1 for il in range(2) for e in range(64))
+        for e in (3, 30, 5):
+            p = c.get(0, e)
+            _check_bytes(qm, recs, (0, e), p, rec)
+        assert c.stats()["misses"] == 3
+    finally:
+        c.close()
+        g.close()
