@@ -324,32 +324,77 @@ __device__ __forceinline__ void q4w_mma(const Q4W<CH> &w, int c0, const int8_t *
     }
 }
 
-// The same product for one or two M tiles (NT) sharing the weight rows,
+// The gate/up product for one or two M tiles (NT) sharing the weight rows,
 // with the 6-bit sub-block scale folded into the weight operand instead of
 // applied to each result: sc = 8*sh + sl with sl, sh in 0..7, so q*sl and
 // q*sh (q <= 15) are int8 values <= 105, and
 //     sum_j sc_j P_j = sum_k a_k (q_k sl_j) + 8 sum_k a_k (q_k sh_j)
-// is two K = 64 MFMA chains over the block (two sub-blocks per MFMA: bytes
-// 0-7 of a lane's operands are its k of sub-block 2t, bytes 8-15 those of
-// 2t+1), exact in int32.  The scaled operands are built once per block (a
-// packed 16-bit multiply per 4 bytes: no byte overflows into the next) and
-// serve every tile; the per-result multiply-adds are gone.  The min term
-// dmin * sum_j m_j * xd * bsum_j takes a precomputed operand,
-// amb[(c*2 + h)*64 + 16*k + p] = xd_c(pair p) * (sum of sub-block 4h + k of
-// pair p's Q8_K block c): one fp32 MFMA pair per block (k = sub-block),
-// accumulated apart from the integer sums.
+// is two K = 64 MFMA chains over the block, exact in int32.  The scaled
+// operands are built once per block (a packed 16-bit multiply per 4 bytes:
+// no byte overflows into the next) and serve every tile; there are no
+// per-result multiply-adds.  The min term dmin * sum_j m_j * xd * bsum_j
+// takes a precomputed operand, amb[(c*2 + h)*64 + 16*k + p] = xd_c(pair p) *
+// (sum of sub-block 4h + k of pair p's Q8_K block c): one fp32 MFMA pair per
+// block (k = sub-block), accumulated apart from the integer sums.
+//
+// The weight bytes are loaded 16 per lane: lane (row lr, quarter q) holds
+// the block header and nibble bytes [16q, 16q+16) and [64+16q, 64+16q+16)
+// of the block's 128, so one load instruction reads 64 contiguous bytes of
+// each of its 16 rows (8-byte pieces, 32 bytes per row per instruction, cap
+// the HBM reads of this pattern at about 3.9 TB/s on this part; 16-byte
+// pieces reach about 5.8).  The MFMA k-assignment follows the bytes: nibble
+// byte j holds k = 64 (j / 32) + j % 32 (low nibble, sub-block 2 (j / 32))
+// and k + 32 (high nibble, sub-block 2 (j / 32) + 1), so for step
+// s = 2 half + hi a lane's 16 operand bytes are k = 128 half + 32 hi +
+// 64 (q >> 1) + 16 (q & 1) + [0, 16), all of sub-block 4 half + 2 (q >> 1) +
+// hi.  Its scale bytes are per lane, and the activation operand is one
+// 16-byte LDS read at the same k.
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t mul_bytes(uint32_t q4, uint32_t m16)
 {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q4) * __builtin_bit_cast(u16x2, m16));
 }
 
+template <int CH>
+struct Q4V {
+    uint4 hdr[CH], qa[CH], qb[CH];
+};
+
+template <int CH>
+__device__ __forceinline__ void q4v_load(Q4V<CH> &w, const uint8_t *wrow, int c0)
+{
+    const int q = lane_id() >> 4;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const uint8_t *blk = wrow + (size_t)(c0 + c) * Q4K_BYTES;
+        w.hdr[c] = ld16(blk);
+        w.qa[c] = ld16(blk + 16 + 16 * q);
+        w.qb[c] = ld16(blk + 80 + 16 * q);
+    }
+}
+
+template <int CH>
+__device__ __forceinline__ void q4v_opaque(Q4V<CH> &w)
+{
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        asm volatile("" : "+v"(w.hdr[c].x), "+v"(w.hdr[c].y), "+v"(w.hdr[c].z), "+v"(w.hdr[c].w));
+        asm volatile("" : "+v"(w.qa[c].x), "+v"(w.qa[c].y), "+v"(w.qa[c].z), "+v"(w.qa[c].w));
+        asm volatile("" : "+v"(w.qb[c].x), "+v"(w.qb[c].y), "+v"(w.qb[c].z), "+v"(w.qb[c].w));
+    }
+}
+
 template <int NB, int CH, int NT>
-__device__ __forceinline__ void q4w_mma_sp(const Q4W<CH> &w, const int8_t *aqA, const float *adA, const float *ambA,
+__device__ __forceinline__ void q4v_mma_sp(const Q4V<CH> &w, const int8_t *aqA, const float *adA, const float *ambA,
                                            float (&rA)[4], const int8_t *aqB, const float *adB, const float *ambB,
                                            float (&rB)[4])
 {
     const int lane = lane_id(), lr = lane & 15, q = lane >> 4;
+    // byte selectors broadcasting sub-block scale byte 2 (q >> 1) (+1) to
+    // both 16-bit halves
+    const uint32_t b0 = 2u * (uint32_t)(q >> 1);
+    const uint32_t sel0 = (b0 * 0x00010001u) | 0x0C000C00u, sel1 = sel0 + 0x00010001u;
+    const int koff = 64 * (q >> 1) + 16 * (q & 1);
     v4f rmA = {0.0f, 0.0f, 0.0f, 0.0f}, rmB = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < CH; c++) {
@@ -369,38 +414,30 @@ __device__ __forceinline__ void q4w_mma_sp(const Q4W<CH> &w, const int8_t *aqA, 
         const uint32_t sh[2] = {(sc_lo >> 3) & 0x07070707u, (sc_hi >> 3) & 0x07070707u};
         v4i a1A = {0, 0, 0, 0}, a2A = a1A, a1B = a1A, a2B = a1A;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            // sub-blocks 2t (low nibbles of group t) and 2t+1 (high); their
-            // scale bytes broadcast to both 16-bit halves by a byte permute
-            const long lo = pack_nib(w.qs[c][t], 0), hi = pack_nib(w.qs[c][t], 1);
-            const uint32_t b0 = (2 * t) & 3, b1 = (2 * t + 1) & 3;
-            const uint32_t s0 = b0 | 0x0C00u | (b0 << 16) | 0x0C000000u, s1 = b1 | 0x0C00u | (b1 << 16) | 0x0C000000u;
-            const uint32_t ml0 = __builtin_amdgcn_perm(0u, sl[t >> 1], s0), ml1 = __builtin_amdgcn_perm(0u, sl[t >> 1], s1);
-            const uint32_t mh0 = __builtin_amdgcn_perm(0u, sh[t >> 1], s0), mh1 = __builtin_amdgcn_perm(0u, sh[t >> 1], s1);
-            const uint32_t l0 = (uint32_t)lo, l1 = (uint32_t)((unsigned long)lo >> 32);
-            const uint32_t h0 = (uint32_t)hi, h1 = (uint32_t)((unsigned long)hi >> 32);
-            const v4i B1 = {(int)mul_bytes(l0, ml0), (int)mul_bytes(l1, ml0), (int)mul_bytes(h0, ml1),
-                            (int)mul_bytes(h1, ml1)};
-            const v4i B2 = {(int)mul_bytes(l0, mh0), (int)mul_bytes(l1, mh0), (int)mul_bytes(h0, mh1),
-                            (int)mul_bytes(h1, mh1)};
+        for (int s = 0; s < 4; s++) {
+            const int half = s >> 1, hi = s & 1;
+            const uint4 src = half ? w.qb[c] : w.qa[c];
+            const uint32_t n0 = hi ? (src.x >> 4) & 0x0F0F0F0Fu : src.x & 0x0F0F0F0Fu;
+            const uint32_t n1 = hi ? (src.y >> 4) & 0x0F0F0F0Fu : src.y & 0x0F0F0F0Fu;
+            const uint32_t n2 = hi ? (src.z >> 4) & 0x0F0F0F0Fu : src.z & 0x0F0F0F0Fu;
+            const uint32_t n3 = hi ? (src.w >> 4) & 0x0F0F0F0Fu : src.w & 0x0F0F0F0Fu;
+            const uint32_t ml = __builtin_amdgcn_perm(0u, sl[half], hi ? sel1 : sel0);
+            const uint32_t mh = __builtin_amdgcn_perm(0u, sh[half], hi ? sel1 : sel0);
+            const v4i B1 = {(int)mul_bytes(n0, ml), (int)mul_bytes(n1, ml), (int)mul_bytes(n2, ml),
+                            (int)mul_bytes(n3, ml)};
+            const v4i B2 = {(int)mul_bytes(n0, mh), (int)mul_bytes(n1, mh), (int)mul_bytes(n2, mh),
+                            (int)mul_bytes(n3, mh)};
+            const int ko = c * QK_K + 128 * half + 32 * hi + koff;
             {
-                const long x0 = *(const long *)(aqA + lr * arow<NB>() + c * QK_K + 64 * t + 8 * q);
-                const long x1 = *(const long *)(aqA + lr * arow<NB>() + c * QK_K + 64 * t + 32 + 8 * q);
-                const v4i av = {(int)(uint32_t)x0, (int)(uint32_t)((unsigned long)x0 >> 32), (int)(uint32_t)x1,
-                                (int)(uint32_t)((unsigned long)x1 >> 32)};
+                const v4i av = *(const v4i *)(aqA + lr * arow<NB>() + ko);
                 a1A = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B1, a1A, 0, 0, 0);
                 a2A = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B2, a2A, 0, 0, 0);
             }
             if constexpr (NT == 2) {
-                const long x0 = *(const long *)(aqB + lr * arow<NB>() + c * QK_K + 64 * t + 8 * q);
-                const long x1 = *(const long *)(aqB + lr * arow<NB>() + c * QK_K + 64 * t + 32 + 8 * q);
-                const v4i av = {(int)(uint32_t)x0, (int)(uint32_t)((unsigned long)x0 >> 32), (int)(uint32_t)x1,
-                                (int)(uint32_t)((unsigned long)x1 >> 32)};
+                const v4i av = *(const v4i *)(aqB + lr * arow<NB>() + ko);
                 a1B = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B1, a1B, 0, 0, 0);
                 a2B = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B2, a2B, 0, 0, 0);
             }
-            // keep each sub-block pair's operands short-lived (the scheduler
-            // would otherwise build all four pairs' ahead and spill)
             __builtin_amdgcn_sched_barrier(0);
         }
         {
@@ -631,8 +668,8 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
                           (size_t)(row0 + lr) * rowb;
     // the weight rows go out first; the pair ids follow as scalar loads
     // (their own counter), so waiting for them leaves the weights in flight
-    Q4W<KH> w;
-    q4w_load(w, wrow, 0);
+    Q4V<KH> w;
+    q4v_load(w, wrow, 0);
     {
         const int wvu = __builtin_amdgcn_readfirstlane(wv);
         const int base = ck.z + 16 * wvu, last = ck.z + npair - 1;
@@ -657,7 +694,7 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
         for (int i = 0; i < 4; i++) r[m][i] = 0.0f;
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) {
-        if (ps > 0) q4w_load(w, wrow, ps * KH);
+        if (ps > 0) q4v_load(w, wrow, ps * KH);
         // tiles in pairs, both buffers staged at once: a pair shares the
         // scaled weight operands
         stage_dma<KH>(s_tok, NBE, ps * KH, xq, xd, xmb, s_aq0, s_ad0, s_mb0);
@@ -666,11 +703,11 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
         for (int mp = 0; mp < MC / PB / 2; mp++) {
             if (2 * mp < mtn) {                // workgroup-uniform
                 __syncthreads();               // the pair's DMA has landed (every wave's)
-                q4w_opaque(w);
+                q4v_opaque(w);
                 if (2 * mp + 1 < mtn)
-                    q4w_mma_sp<KH, KH, 2>(w, s_aq0, s_ad0, s_mb0, r[2 * mp], s_aq1, s_ad1, s_mb1, r[2 * mp + 1]);
+                    q4v_mma_sp<KH, KH, 2>(w, s_aq0, s_ad0, s_mb0, r[2 * mp], s_aq1, s_ad1, s_mb1, r[2 * mp + 1]);
                 else
-                    q4w_mma_sp<KH, KH, 1>(w, s_aq0, s_ad0, s_mb0, r[2 * mp], s_aq1, s_ad1, s_mb1, r[2 * mp + 1]);
+                    q4v_mma_sp<KH, KH, 1>(w, s_aq0, s_ad0, s_mb0, r[2 * mp], s_aq1, s_ad1, s_mb1, r[2 * mp + 1]);
                 if (2 * mp + 2 < mtn) {
                     __syncthreads();           // both buffers read: stage the next pair
                     stage_dma<KH>(s_tok + PB * (2 * mp + 2), NBE, ps * KH, xq, xd, xmb, s_aq0, s_ad0, s_mb0);
