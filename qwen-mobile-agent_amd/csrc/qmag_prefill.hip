@@ -463,107 +463,116 @@ __device__ __forceinline__ void q4v_mma_sp(const Q4V<CH> &w, const int8_t *aqA, 
 }
 
 // ------------------------------------------------------- Q6_K x Q8_K tile --
-// Same contract for Q6_K rows; one MFMA per 16-wide group, whose 16 values
-// sit in lanes q = 0, 1 (k 0..15); lanes q = 2, 3 carry zero weights.  For
-// (block, half n, lane half hl) a lane q < 2 holds the ql bytes of quarters
-// Q = 0/2 and 1/3 (low/high nibbles) and the qh bytes of all four.
+// Same contract for Q6_K rows (scales per 16 values, so each MFMA result
+// must hold one 16-value group).  A lane (row lr, quarter q) loads 16-byte
+// pieces: ql bytes [16q, 16q+16) of each half n (64 bytes per half), the qh
+// bytes [16 (q & 1), +16) of each half, the 16 scales and d -- 64 contiguous
+// bytes of each row per ql load instruction.  Per half, ql byte l' = 16q + i
+// holds element 32 Q + l (l = l' % 32 = 16 (q & 1) + i) with Q = q >> 1 in
+// its low nibble and Q = (q >> 1) + 2 in its high nibble, whose top two bits
+// are bits 2Q, 2Q+1 of qh byte l (src/quants.c:56-69): so each lane holds
+// four whole groups per block, g = 2n + hi, of scale 8n + 2Q + (q & 1).
+// One v_mfma_i32_16x16x64_i8 per (group slot g, lane quarter t): every lane
+// supplies its slot-g group as the weight operand, and only lanes q = t
+// supply activations (the others read a zero row), so the result is the dot
+// of quarter t's group alone, which its scale then multiplies.
 template <int NB>
-struct Q6W {
-    uint2 ql[NB][2][2][2], qh[NB][2][2];     // [block][n][hl][Q & 1], [block][n][hl]
+struct Q6V {
+    uint4 ql[NB][2], qh[NB][2];                // [block][half]
     uint4 sc16[NB];
     uint32_t dbits[NB];
 };
 
 template <int NB>
-__device__ __forceinline__ void q6w_load(Q6W<NB> &w, const uint8_t *wrow)
+__device__ __forceinline__ void q6v_load(Q6V<NB> &w, const uint8_t *wrow)
 {
-    const int q = lane_id() >> 4, qq = q & 1;
+    const int q = lane_id() >> 4;
 #pragma unroll
     for (int ib = 0; ib < NB; ib++) {
         const uint8_t *blk = wrow + (size_t)ib * Q6K_BYTES;
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            w.ql[ib][n] = ld16(blk + 64 * n + 16 * q);
+            w.qh[ib][n] = ld16(blk + 128 + 32 * n + 16 * (q & 1));
+        }
         w.sc16[ib] = ld16(blk + 192);
         w.dbits[ib] = ld2(blk + 208);
-#pragma unroll
-        for (int n = 0; n < 2; n++)
-#pragma unroll
-            for (int hl = 0; hl < 2; hl++) {
-                const int l0 = 16 * hl + 8 * qq;
-                if (q < 2) {
-                    w.ql[ib][n][hl][0] = ld8(blk + 64 * n + l0);
-                    w.ql[ib][n][hl][1] = ld8(blk + 64 * n + 32 + l0);
-                    w.qh[ib][n][hl] = ld8(blk + 128 + 32 * n + l0);
-                } else {
-                    w.ql[ib][n][hl][0] = w.ql[ib][n][hl][1] = w.qh[ib][n][hl] = make_uint2(0, 0);
-                }
-            }
     }
 }
 
-// The same rows with every group's MFMA operand built once (centred 6-bit
-// values, lanes q = 2, 3 zero): a workgroup that runs several M tiles
-// against the same rows unpacks them once instead of per tile.
+// the four groups of each block as centred int8 operands
 template <int NB>
-struct Q6B {
-    long b[NB][16];
+struct Q6VB {
+    v4i b[NB][4];
     uint4 sc16[NB];
     uint32_t dbits[NB];
 };
 
 template <int NB>
-__device__ __forceinline__ void q6b_unpack(Q6B<NB> &u, const Q6W<NB> &w)
+__device__ __forceinline__ void q6v_unpack(Q6VB<NB> &u, const Q6V<NB> &w)
 {
     const int q = lane_id() >> 4;
+    const uint32_t sh0 = 2u * (uint32_t)(q >> 1);  // 2Q of the low-nibble group
 #pragma unroll
     for (int ib = 0; ib < NB; ib++) {
         u.sc16[ib] = w.sc16[ib];
         u.dbits[ib] = w.dbits[ib];
 #pragma unroll
-        for (int gg = 0; gg < 16; gg++) {
-            const int n = gg >> 3, Q = (gg >> 1) & 3, hl = gg & 1;
-            const uint2 l8 = w.ql[ib][n][hl][Q & 1], h8 = w.qh[ib][n][hl];
-            const uint32_t lo0 = Q < 2 ? l8.x & 0x0F0F0F0Fu : (l8.x >> 4) & 0x0F0F0F0Fu;
-            const uint32_t lo1 = Q < 2 ? l8.y & 0x0F0F0F0Fu : (l8.y >> 4) & 0x0F0F0F0Fu;
-            const uint32_t hb0 = ((h8.x >> (2 * Q)) & 0x03030303u) << 4;
-            const uint32_t hb1 = ((h8.y >> (2 * Q)) & 0x03030303u) << 4;
-            u.b[ib][gg] = q < 2 ? (long)(((unsigned long long)q6_center(lo1 | hb1) << 32) | q6_center(lo0 | hb0)) : 0;
+        for (int g = 0; g < 4; g++) {
+            const int n = g >> 1, hi = g & 1;
+            const uint32_t L[4] = {w.ql[ib][n].x, w.ql[ib][n].y, w.ql[ib][n].z, w.ql[ib][n].w};
+            const uint32_t H[4] = {w.qh[ib][n].x, w.qh[ib][n].y, w.qh[ib][n].z, w.qh[ib][n].w};
+            const uint32_t sh = sh0 + 4u * hi;
+            int v[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t lo4 = hi ? (L[k] >> 4) & 0x0F0F0F0Fu : L[k] & 0x0F0F0F0Fu;
+                v[k] = (int)q6_center(lo4 | (((H[k] >> sh) & 0x03030303u) << 4));
+            }
+            u.b[ib][g] = v4i{v[0], v[1], v[2], v[3]};
         }
     }
 }
 
 template <int NB>
-__device__ __forceinline__ void q6b_opaque(Q6B<NB> &u)
+__device__ __forceinline__ void q6v_opaque(Q6VB<NB> &u)
 {
 #pragma unroll
     for (int ib = 0; ib < NB; ib++)
 #pragma unroll
-        for (int gg = 0; gg < 16; gg++) asm volatile("" : "+v"(u.b[ib][gg]));
+        for (int g = 0; g < 4; g++) asm volatile("" : "+v"(u.b[ib][g]));
 }
 
+// abase[t] = this lane's activation row (pair lr) when q == t, else a zero
+// row of the same length
 template <int NB>
-__device__ __forceinline__ void q6b_mma(const Q6B<NB> &u, const int8_t *aq, const float *ad, float (&r)[4])
+__device__ __forceinline__ void q6v_mma(const Q6VB<NB> &u, const int8_t *const (&abase)[4], const float *ad,
+                                        float (&r)[4])
 {
-    const int lane = lane_id(), lr = lane & 15, q = lane >> 4, qq = q & 1;
+    const int q = lane_id() >> 4;
 #pragma unroll
     for (int ib = 0; ib < NB; ib++) {
         int acc[4] = {0, 0, 0, 0};
         const uint32_t scw[4] = {u.sc16[ib].x, u.sc16[ib].y, u.sc16[ib].z, u.sc16[ib].w};
 #pragma unroll
-        for (int h4 = 0; h4 < 4; h4++) {
-            // four groups' MFMAs back to back, then their scale multiply-adds
+        for (int g = 0; g < 4; g++) {
+            const int n = g >> 1, hi = g & 1;
+            // four MFMAs back to back, then their scale multiply-adds
             v4i p[4];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int gg = 4 * h4 + g, n = gg >> 3, Q = (gg >> 1) & 3, hl = gg & 1;
-                const long a = *(const long *)(aq + lr * arow<NB>() + ib * QK_K + 128 * n + 32 * Q + 16 * hl + 8 * qq);
-                p[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, u.b[ib][gg], v4i{0, 0, 0, 0}, 0, 0, 0);
+            for (int t = 0; t < 4; t++) {
+                const int Q = (t >> 1) + 2 * hi;
+                const v4i a = *(const v4i *)(abase[t] + ib * QK_K + 128 * n + 32 * Q + 16 * (t & 1));
+                p[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, u.b[ib][g], v4i{0, 0, 0, 0}, 0, 0, 0);
             }
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int sc = (int)(int8_t)((scw[h4] >> (8 * g)) & 255);
-                acc[0] = __mul24(sc, p[g][0]) + acc[0];
-                acc[1] = __mul24(sc, p[g][1]) + acc[1];
-                acc[2] = __mul24(sc, p[g][2]) + acc[2];
-                acc[3] = __mul24(sc, p[g][3]) + acc[3];
+            for (int t = 0; t < 4; t++) {
+                const int si = 8 * n + 2 * ((t >> 1) + 2 * hi) + (t & 1);
+                const int sc = (int)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 255);
+                acc[0] = __mul24(sc, p[t][0]) + acc[0];
+                acc[1] = __mul24(sc, p[t][1]) + acc[1];
+                acc[2] = __mul24(sc, p[t][2]) + acc[2];
+                acc[3] = __mul24(sc, p[t][3]) + acc[3];
             }
         }
         const float d = h2f(u.dbits[ib]);
@@ -753,67 +762,56 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
 constexpr int DN_ROWS = 64;
 
 // stage rows[0 .. 16*mtn) of Q8_K(h) (NB super-blocks each) into
-// aq[p][arow<NB>()] and their scales into ad[p / 16][block][p % 16]: one
-// 256-byte DMA per (pair, block), one dword per lane; every pair slot has a
-// valid row (absent pairs repeat the chunk's first), so no DMA is skipped
+// aq[p][arow<NB>()] and their scales into ad[p / 16][block][p % 16]: 16-byte
+// loads into registers (Staged::load), written to LDS once they arrive
+// (Staged::store); per-dword DMAs into LDS, four times the instructions,
+// made the staging of a 64-pair chunk cost about 4 us more than that of a
+// 16-pair one.  Every pair slot has a valid row (absent pairs repeat the
+// chunk's first).
 template <int NB>
-__device__ __forceinline__ void stage_rows_dma(const int *rows, int mtn, const int8_t *hq, const float *hd,
-                                               int8_t *aq, float *ad)
-{
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
-    const int n = PB * mtn * NB;
-    for (int i = wv; i < n; i += 4) {          // wave-uniform
-        const int p = i / NB, ib = i % NB;
-        __builtin_amdgcn_global_load_lds(
-            (const QMAG_GLOBAL void *)(hq + (size_t)rows[p] * (NB * QK_K) + ib * QK_K + lane * 4),
-            (__attribute__((address_space(3))) void *)(aq + p * arow<NB>() + ib * QK_K), 4, 0, 0);
-    }
-    for (int s0 = 64 * wv; s0 < n; s0 += 256) {
-        const int sl = s0 + lane, mt = sl / (NB * PB), ib = (sl / PB) % NB, p = PB * mt + sl % PB;
-        if (sl < n)
-            __builtin_amdgcn_global_load_lds((const QMAG_GLOBAL void *)(hd + (size_t)rows[min(p, PB * mtn - 1)] * NB + ib),
-                                             (__attribute__((address_space(3))) void *)(ad + s0), 4, 0, 0);
-    }
-}
+struct Staged {
+    static constexpr int PPR = NB * QK_K / 16;     // 16-byte pieces per row
+    static constexpr int IT = MC * PPR / 256;      // pieces per thread, full chunk
+    uint4 v[IT];
+    float sv;
 
-template <int NBF, int TD>
-__device__ __forceinline__ void down_tiles(const uint8_t *D, const int8_t *aq, const float *ad, int mtn,
-                                           float (&r)[MC / PB][4])
-{
-    if constexpr (TD == QMAG_TYPE_Q6_K) {
-        Q6B<NBF> u;
-        {
-            Q6W<NBF> w;
-            q6w_load(w, D);
-            q6b_unpack(u, w);
+    __device__ __forceinline__ void load(const int *rows, int mtn, const int8_t *hq, const float *hd)
+    {
+        const int t = (int)threadIdx.x, n = PB * mtn * PPR;
+#pragma unroll
+        for (int k = 0; k < IT; k++) {
+            const int i = t + 256 * k, p = i / PPR, pc = i % PPR;
+            if (k * 256 < n) v[k] = ld16((const uint8_t *)hq + (size_t)rows[p] * (NB * QK_K) + pc * 16);
         }
-        __syncthreads();                       // the staging DMA has landed (every wave's)
-#pragma unroll
-        for (int m = 0; m < MC / PB; m++)
-            if (m < mtn) {
-                q6b_opaque(u);
-                q6b_mma<NBF>(u, aq + PB * m * arow<NBF>(), ad + m * NBF * PB, r[m]);
-            }
-    } else {
-        Q4W<NBF> w;
-        q4w_load(w, D, 0);
-        __syncthreads();
-#pragma unroll
-        for (int m = 0; m < MC / PB; m++)
-            if (m < mtn) {
-                q4w_opaque(w);
-                q4w_mma<NBF, NBF>(w, 0, aq + PB * m * arow<NBF>(), ad + m * NBF * PB, r[m]);
-            }
+        sv = 0.0f;
+        if (t < PB * mtn * NB) {
+            const int mt = t / (NB * PB), ib = (t / PB) % NB, p = PB * mt + t % PB;
+            sv = ldg(hd + (size_t)rows[p] * NB + ib);
+        }
     }
-}
+    __device__ __forceinline__ void store(int mtn, int8_t *aq, float *ad) const
+    {
+        const int t = (int)threadIdx.x, n = PB * mtn * PPR;
+#pragma unroll
+        for (int k = 0; k < IT; k++) {
+            const int i = t + 256 * k, p = i / PPR, pc = i % PPR;
+            if (k * 256 < n) *(uint4 *)(aq + p * arow<NB>() + pc * 16) = v[k];
+        }
+        if (t < PB * mtn * NB) ad[t] = sv;
+    }
+};
 
+#ifndef QMAG_DN_WPC
+#define QMAG_DN_WPC 2
+#endif
 template <int NBF>
-__global__ __launch_bounds__(256, 2) void down_rows_kernel(
+__global__ __launch_bounds__(256, QMAG_DN_WPC) void down_rows_kernel(
     const uint8_t *__restrict__ down_exps, int t_down, const uint8_t *__restrict__ down_sh, int t_down_sh,
     int E, int N, const int4 *__restrict__ chunk, const int *__restrict__ perm, const int8_t *__restrict__ hq,
     const float *__restrict__ hd, float *__restrict__ y)
 {
     __shared__ __align__(16) int8_t s_aq[MC * arow<NBF>()];
+    __shared__ __align__(16) int8_t s_zero[arow<NBF>()];     // the Q6_K MFMAs' inactive activation lanes
     __shared__ __align__(16) float s_ad[MC * NBF];
     __shared__ int s_pair[MC], s_row[MC];
     const int rblocks = N / DN_ROWS;
@@ -821,11 +819,21 @@ __global__ __launch_bounds__(256, 2) void down_rows_kernel(
     const int4 ck = chunk[u];
     if (ck.x < 0) return;
     const int e = ck.x, npair = ck.y, mtn = (npair + PB - 1) / PB;
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), q = lane >> 4;
-    const int row = rb * DN_ROWS + wv * 16 + (lane & 15);
-    // pair ids by scalar loads (see gateup_rows_kernel); rows of absent
-    // pairs repeat the first pair's
-    {
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), lr = lane & 15, q = lane >> 4;
+    const int row = rb * DN_ROWS + wv * 16 + lr;
+    const int td = e < E ? t_down : t_down_sh;
+    const size_t rowb = (size_t)NBF * (td == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES);
+    const uint8_t *D = (e < E ? down_exps + (size_t)e * N * rowb : down_sh) + row * rowb;
+    float r[MC / PB][4];
+#pragma unroll
+    for (int m = 0; m < MC / PB; m++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[m][i] = 0.0f;
+    // the wave's 16 weight rows are requested first; the pair ids follow as
+    // scalar loads (rows of absent pairs repeat the first pair's), then the
+    // chunk's Q8_K(h) rows, whose loads drain before the weights' in the
+    // load counter's order
+    auto ids = [&]() __attribute__((always_inline)) {
         const int wvu = __builtin_amdgcn_readfirstlane(wv);
         const int base = ck.z + 16 * wvu, last = ck.z + npair - 1;
         int v[16];
@@ -839,19 +847,45 @@ __global__ __launch_bounds__(256, 2) void down_rows_kernel(
             s_pair[16 * wvu + lane] = mine;
             s_row[16 * wvu + lane] = mine >= 0 ? mine : perm[ck.z];
         }
+        for (int i = (int)threadIdx.x; i < arow<NBF>() / 16; i += 256) ((uint4 *)s_zero)[i] = make_uint4(0, 0, 0, 0);
+        __syncthreads();
+    };
+    Staged<NBF> stg;
+    if (td == QMAG_TYPE_Q6_K) {
+        Q6VB<NBF> ub;
+        {
+            Q6V<NBF> w;
+            q6v_load(w, D);
+            ids();
+            stg.load(s_row, mtn, hq, hd);
+            stg.store(mtn, s_aq, s_ad);
+            q6v_unpack(ub, w);
+        }
+        __syncthreads();                       // every wave's staged rows are in LDS
+        const int8_t *arow_m = s_aq + lr * arow<NBF>();
+#pragma unroll
+        for (int m = 0; m < MC / PB; m++)
+            if (m < mtn) {
+                q6v_opaque(ub);
+                const int8_t *const abase[4] = {q == 0 ? arow_m : s_zero, q == 1 ? arow_m : s_zero,
+                                                q == 2 ? arow_m : s_zero, q == 3 ? arow_m : s_zero};
+                q6v_mma<NBF>(ub, abase, s_ad + m * NBF * PB, r[m]);
+                arow_m += PB * arow<NBF>();
+            }
+    } else {
+        Q4W<NBF> w;
+        q4w_load(w, D, 0);
+        ids();
+        stg.load(s_row, mtn, hq, hd);
+        stg.store(mtn, s_aq, s_ad);
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < MC / PB; m++)
+            if (m < mtn) {
+                q4w_opaque(w);
+                q4w_mma<NBF, NBF>(w, 0, s_aq + PB * m * arow<NBF>(), s_ad + m * NBF * PB, r[m]);
+            }
     }
-    __syncthreads();
-    stage_rows_dma<NBF>(s_row, mtn, hq, hd, s_aq, s_ad);
-    const int td = e < E ? t_down : t_down_sh;
-    const size_t rowb = (size_t)NBF * (td == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES);
-    const uint8_t *D = (e < E ? down_exps + (size_t)e * N * rowb : down_sh) + row * rowb;
-    float r[MC / PB][4];
-#pragma unroll
-    for (int m = 0; m < MC / PB; m++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) r[m][i] = 0.0f;
-    if (td == QMAG_TYPE_Q6_K) down_tiles<NBF, QMAG_TYPE_Q6_K>(D, s_aq, s_ad, mtn, r);
-    else down_tiles<NBF, QMAG_TYPE_Q4_K>(D, s_aq, s_ad, mtn, r);
 #pragma unroll
     for (int m = 0; m < MC / PB; m++)
 #pragma unroll
