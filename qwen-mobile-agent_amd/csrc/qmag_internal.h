@@ -89,7 +89,8 @@ int moe_ffn(const qmag_moe_layer *L, const float *x, float *out, int T, const fl
 int moe_check_layer(const qmag_moe_layer *L, bool need_exps = true);
 
 // grouped prefill (qmag_prefill.hip)
-int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *logits, hipStream_t s);
+// part[kc][T][E]: x . Wr^T over 256-wide k chunk kc (no bias)
+int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *part, hipStream_t s);
 int moe_grouped(const qmag_moe_layer *L, int T, const int *sel, const float *w, const float *gs,
                 const int8_t *xq, const float *xd, const float *xmb, float *h, int8_t *hq, float *hd,
                 int16_t *hs, const float *resid, float *out, hipStream_t s);

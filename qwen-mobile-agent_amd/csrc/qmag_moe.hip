@@ -70,7 +70,8 @@ __device__ __forceinline__ void tk_cswap(float (&p)[4], int (&id)[4], int a, int
 // a pick is one wave max over the lane heads, a ballot for the lanes holding
 // it (more than one only on an exact tie, then the lowest index among them)
 // and a shift of the winning lane's list.
-__global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits,
+__global__ __launch_bounds__(256) void topk_kernel(float *__restrict__ logits, int npart, size_t pstride,
+                                                   const float *__restrict__ lbias,
                                                    const float *__restrict__ x,
                                                    const float *__restrict__ wsh, int N, int E,
                                                    int K, int *__restrict__ sel,
@@ -92,11 +93,32 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
         xv[i] = ((const float4 *)(x + (size_t)t * N + b * QK_K))[lane];
         gw[i] = ((const float4 *)(wsh + b * QK_K))[lane];
     }
+    // logits[t][e] = the npart chunk partials summed in order, then the bias
     float l[4];
     if (wv == 0) {
         const float *lg = logits + (size_t)t * E;
 #pragma unroll
         for (int j = 0; j < 4; j++) l[j] = lg[min(lane + 64 * j, E - 1)];
+        // every partial requested before the first add (npart <= 16)
+        float pv[15][4];
+#pragma unroll
+        for (int p = 1; p < 16; p++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) pv[p - 1][j] = p < npart ? lg[p * pstride + min(lane + 64 * j, E - 1)] : 0.0f;
+#pragma unroll
+        for (int p = 1; p < 16; p++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (p < npart) l[j] += pv[p - 1][j];
+        if (lbias)
+#pragma unroll
+            for (int j = 0; j < 4; j++) l[j] = l[j] + lbias[min(lane + 64 * j, E - 1)];
+        // the final logits replace chunk 0's partial (read only here), so
+        // the buffer reads as logits[T][E] afterwards
+        if (npart > 1 || lbias)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (lane + 64 * j < E) logits[(size_t)t * E + lane + 64 * j] = l[j];
     }
 
     // Q8_K of x[t] (one wave per 256-block) and the shared gate's
@@ -395,7 +417,7 @@ static int moe_ws(const qmag_moe_layer *L, int T, MoeWs &ws)
 #define WS(field, type, slot, count)                                              \
     ws.field = (type *)workspace(slot, sizeof(type) * (size_t)(count), &st);      \
     if (st) return st;
-    WS(logits, float, WS_LOGITS, (size_t)T * E);
+    WS(logits, float, WS_LOGITS, (size_t)T * E * (N / QK_K));   // the grouped router's chunk partials
     WS(sel, int, WS_SEL, (size_t)T * K);
     WS(w, float, WS_W, (size_t)T * K);
     WS(gs, float, WS_GS, T);
@@ -502,8 +524,10 @@ static int route_tokens(const qmag_moe_layer *L, const float *x, int T, bool gro
     }
     prof_end(PROF_ROUTER, s);
     prof_begin(PROF_TOPK, s);
-    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(256), 0, s, ws.logits, x, L->gate_inp_shexp, N,
-                       E, K, ws.sel, ws.w, ws.gs, ws.xq, ws.xd, ws.xs, grouped ? ws.xmb : nullptr);
+    // the grouped router leaves one partial per 256-wide k chunk and no bias
+    hipLaunchKernelGGL(topk_kernel, dim3(T), dim3(256), 0, s, ws.logits, grouped ? N / 256 : 1, (size_t)T * E,
+                       grouped ? L->router_bias : nullptr, x, L->gate_inp_shexp, N, E, K, ws.sel, ws.w, ws.gs,
+                       ws.xq, ws.xd, ws.xs, grouped ? ws.xmb : nullptr);
     prof_end(PROF_TOPK, s);
     return QMAG_OK;
 }

@@ -1,7 +1,8 @@
 // qmag_prefill.hip -- the MoE FFN layer for a batch of tokens (prefill,
 // src/nn.c:509-649 with T > 1) as a grouped expert GEMM on int8 MFMA.
 //
-//   router_mfma_kernel   logits[T][E] = x . Wr^T (+ synthetic bias), fp32 MFMA
+//   router_tile_kernel   per 256-wide k chunk, part[kc][T][E] = x . Wr^T, fp32
+//                        MFMA; topk_kernel sums the chunks and adds the bias
 //   topk_kernel          (qmag_moe.hip) softmax/top-k, Q8_K(x), shared gate
 //   group_kernel         (token, slot) pairs bucketed by expert; the shared
 //                        expert is bucket E with one pair per token
@@ -44,61 +45,70 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int PB = 16;            // pairs per MFMA tile (the 16-wide M side)
 
 // --------------------------------------------------------------- router --
-// One workgroup per 16 tokens x 16 experts with W = N/256 waves; wave w
-// owns k = [256w, 256w + 256).  Lane group q takes float4 4u+q of that
-// range in request u, so the four lanes of one row read 64 contiguous bytes
-// per request (16 cache lines per request, not 64).  Each lane issues its 16
-// float4 of one x row and of one router row at once (no load waits on
-// another's round trip) and feeds them to four independent accumulators.
-// Rows past T or E are clamped to the last one: they only reach output
-// elements that are not stored.  The waves' partial tiles are summed
-// through LDS in a fixed order.
-template <int W>
-__global__ __launch_bounds__(64 * W) void router_mfma_kernel(const float *__restrict__ Wr,
-                                                             const float *__restrict__ bias,
-                                                             const float *__restrict__ x, int N, int E,
-                                                             int T, float *__restrict__ logits)
+// grid: (T / 64) x (E / 64) x (N / 256), 512 threads; a workgroup = 64 tokens
+// x 64 experts x one 256-wide k chunk kc.  The 64 x rows and 64 router rows
+// of the chunk are staged in LDS by DMA (one 1 KB row per instruction,
+// rows padded by 16 bytes so the 16 rows one read touches start 4 banks
+// apart), and wave w computes tokens 16 (w & 3) .. +16 against experts
+// 32 (w >> 2) .. +32 as two 16 x 16 tiles.  Each tile's product over the
+// chunk is 64 v_mfma_f32_16x16x4f32 into four accumulators (lane quarter q
+// takes k = 16 u + 4 q .. +4 of step u, accumulator u % 4), summed as
+// (a0 + a1) + (a2 + a3) and stored as the chunk's partial
+// part[kc][token][expert]; topk_kernel adds the chunks in order and then
+// the bias.  Each x and router row is read by 4 (not 16) workgroups, from
+// LDS instead of registers, so one workgroup per CU suffices.  Rows past T or
+// E are clamped to the last one: they only reach outputs that are not
+// stored.
+constexpr int RT_ROWS = 64;                    // tokens (experts) per workgroup
+constexpr int RT_STRIDE = 256 + 4;             // padded LDS row, floats
+__global__ __launch_bounds__(512) void router_tile_kernel(const float *__restrict__ Wr,
+                                                          const float *__restrict__ x, int N, int E, int T,
+                                                          float *__restrict__ part)
 {
-    constexpr int V = 16;                      // float4 per lane and operand
-    __shared__ v4f s_red[W > 1 ? W - 1 : 1][64];
-    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
-    const int eblocks = (E + 15) / 16;
-    const int tb = (int)blockIdx.x / eblocks, eb = (int)blockIdx.x % eblocks;
-    const int tok = min(tb * 16 + (lane & 15), T - 1), e = min(eb * 16 + (lane & 15), E - 1), q = lane >> 4;
-    const float4 *xr = (const float4 *)(x + (size_t)tok * N) + 4 * V * wv + q;
-    const float4 *wr = (const float4 *)(Wr + (size_t)e * N) + 4 * V * wv + q;
-    float4 a[V], b[V];
+    __shared__ __align__(16) float s_x[RT_ROWS * RT_STRIDE], s_w[RT_ROWS * RT_STRIDE];
+    const int tb = (int)blockIdx.x, eb = (int)blockIdx.y, kc = (int)blockIdx.z;
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), lr = lane & 15, q = lane >> 4;
 #pragma unroll
-    for (int u = 0; u < V; u++) {
-        a[u] = xr[4 * u];
-        b[u] = wr[4 * u];
+    for (int i = 0; i < RT_ROWS / 8; i++) {
+        const int r = wv + 8 * i;
+        const int tok = min(tb * RT_ROWS + r, T - 1), e = min(eb * RT_ROWS + r, E - 1);
+        __builtin_amdgcn_global_load_lds((const QMAG_GLOBAL void *)(x + (size_t)tok * N + kc * 256 + lane * 4),
+                                         (__attribute__((address_space(3))) void *)(s_x + r * RT_STRIDE), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const QMAG_GLOBAL void *)(Wr + (size_t)e * N + kc * 256 + lane * 4),
+                                         (__attribute__((address_space(3))) void *)(s_w + r * RT_STRIDE), 16, 0, 0);
     }
-    __builtin_amdgcn_sched_barrier(0);         // every request issued before the first MFMA
-    v4f acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
-                  {0.0f, 0.0f, 0.0f, 0.0f}};
+    __syncthreads();
+    const int t0 = 16 * (wv & 3), e0 = 32 * (wv >> 2);
+    const float *xa = s_x + (t0 + lr) * RT_STRIDE + 4 * q;
+    const float *wa = s_w + (e0 + lr) * RT_STRIDE + 4 * q;
+    v4f acc[2][4];
 #pragma unroll
-    for (int u = 0; u < V; u++) {
-        v4f &c = acc[u & 3];
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, c, 0, 0, 0);
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[j][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+        const float4 a = *(const float4 *)(xa + 16 * u);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const float4 b = *(const float4 *)(wa + 16 * RT_STRIDE * j + 16 * u);
+            v4f &c = acc[j][u & 3];
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
+        }
     }
-    const v4f part = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    if (W > 1) {
-        if (wv > 0) s_red[wv - 1][lane] = part;
-        __syncthreads();
-        if (wv > 0) return;
-    }
-    v4f sum = part;
+    // lane holds tile rows 4q + i (tokens) x column lr (expert)
 #pragma unroll
-    for (int w = 0; w < W - 1; w++) sum += s_red[w][lane];
-    // lane holds logits[tb*16 + 4q + i][eb*16 + lane%16]
-    const int eo = eb * 16 + (lane & 15);
+    for (int j = 0; j < 2; j++) {
+        const v4f sum = (acc[j][0] + acc[j][1]) + (acc[j][2] + acc[j][3]);
+        const int eo = eb * RT_ROWS + e0 + 16 * j + lr;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int to = tb * 16 + 4 * q + i;
-        if (to < T && eo < E) logits[(size_t)to * E + eo] = bias ? sum[i] + bias[eo] : sum[i];
+        for (int i = 0; i < 4; i++) {
+            const int to = tb * RT_ROWS + t0 + 4 * q + i;
+            if (to < T && eo < E) part[((size_t)kc * T + to) * E + eo] = sum[i];
+        }
     }
 }
 
@@ -937,21 +947,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 }
 
 // ------------------------------------------------------------------ host --
-int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *logits, hipStream_t s)
+int launch_router_mfma(const qmag_moe_layer *L, const float *x, int T, float *part, hipStream_t s)
 {
     const int N = L->n_embd, E = L->n_expert;
-    const int tiles = ((T + 15) / 16) * ((E + 15) / 16);
-    auto go = [&](auto kern, int W) {
-        hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * W), 0, s, L->gate_inp, L->router_bias, x, N, E, T, logits);
-    };
-    switch (N / QK_K) {                 // N = 256 * W, W a power of two up to 16 (moe_check_layer)
-    case 1: go(router_mfma_kernel<1>, 1); break;
-    case 2: go(router_mfma_kernel<2>, 2); break;
-    case 4: go(router_mfma_kernel<4>, 4); break;
-    case 8: go(router_mfma_kernel<8>, 8); break;
-    case 16: go(router_mfma_kernel<16>, 16); break;
-    default: return fail(QMAG_ERR_ARG, "router: n_embd=%d", N);
-    }
+    if (N % 256) return fail(QMAG_ERR_ARG, "router: n_embd=%d", N);
+    hipLaunchKernelGGL(router_tile_kernel, dim3((T + RT_ROWS - 1) / RT_ROWS, (E + RT_ROWS - 1) / RT_ROWS, N / 256),
+                       dim3(512), 0, s, L->gate_inp, x, N, E, T, part);
     QMAG_HIP(hipGetLastError());
     return QMAG_OK;
 }
