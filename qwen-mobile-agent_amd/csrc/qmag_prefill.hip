@@ -839,23 +839,23 @@ __global__ __launch_bounds__(256, QMAG_DN_WPC) void down_rows_kernel(
     for (int m = 0; m < MC / PB; m++)
 #pragma unroll
         for (int i = 0; i < 4; i++) r[m][i] = 0.0f;
-    // the wave's 16 weight rows are requested first; the pair ids follow as
-    // scalar loads (rows of absent pairs repeat the first pair's), then the
-    // chunk's Q8_K(h) rows, whose loads drain before the weights' in the
-    // load counter's order
-    auto ids = [&]() __attribute__((always_inline)) {
-        const int wvu = __builtin_amdgcn_readfirstlane(wv);
-        const int base = ck.z + 16 * wvu, last = ck.z + npair - 1;
-        int v[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++) v[k] = perm[min(base + k, last)];
-        int mine = -1;
-#pragma unroll
-        for (int k = 0; k < 16; k++)
-            if (lane == k && 16 * wvu + k < npair) mine = v[k];
+    // the pair ids go out first, one vector load per pair (rows of absent
+    // pairs repeat the first pair's), then the wave's 16 weight rows, then,
+    // once the ids are in LDS, the chunk's Q8_K(h) rows: each wait leaves
+    // the later requests in flight (the load counter drains in issue order).
+    // Requesting the ids after the rows made them wait behind the rows
+    // (67.0 against 64.9 us per layer).
+    const int idx = 16 * wv + lane;
+    int mine = -1, first = 0;
+    auto ids_load = [&]() __attribute__((always_inline)) {
+        if (lane < 16 && idx < npair) mine = perm[ck.z + idx];
+        first = perm[ck.z];
+        asm volatile("" ::: "memory");
+    };
+    auto ids_store = [&]() __attribute__((always_inline)) {
         if (lane < 16) {
-            s_pair[16 * wvu + lane] = mine;
-            s_row[16 * wvu + lane] = mine >= 0 ? mine : perm[ck.z];
+            s_pair[idx] = mine;
+            s_row[idx] = mine >= 0 ? mine : first;
         }
         for (int i = (int)threadIdx.x; i < arow<NBF>() / 16; i += 256) ((uint4 *)s_zero)[i] = make_uint4(0, 0, 0, 0);
         __syncthreads();
@@ -865,8 +865,9 @@ __global__ __launch_bounds__(256, QMAG_DN_WPC) void down_rows_kernel(
         Q6VB<NBF> ub;
         {
             Q6V<NBF> w;
+            ids_load();
             q6v_load(w, D);
-            ids();
+            ids_store();
             stg.load(s_row, mtn, hq, hd);
             stg.store(mtn, s_aq, s_ad);
             q6v_unpack(ub, w);
@@ -884,8 +885,9 @@ __global__ __launch_bounds__(256, QMAG_DN_WPC) void down_rows_kernel(
             }
     } else {
         Q4W<NBF> w;
+        ids_load();
         q4w_load(w, D, 0);
-        ids();
+        ids_store();
         stg.load(s_row, mtn, hq, hd);
         stg.store(mtn, s_aq, s_ad);
         __syncthreads();
