@@ -596,10 +596,12 @@ __device__ __forceinline__ void q6v_mma(const Q6VB<NB> &u, const int8_t *const (
 
 // --------------------------------------------- gate / up, rows resident --
 // grid: (max MC-pair chunks) x (F / GR_ROWS); a workgroup = one chunk of up
-// to 64 pairs of one bucket x 32 rows of h: waves 0-1 hold 16 gate rows
-// each, waves 2-3 the same rows of up.  A wave loads its 16 rows whole
-// (KH super-blocks = 1152 contiguous bytes per row for n_embd 2048) into
-// registers at once -- HBM sees each row read as one burst -- and keeps
+// to 64 pairs of one bucket x 32 rows of h.  Wave w holds 8 of them: the gate
+// rows in lanes 0-7 of its 16-row tile and the same rows of up in lanes
+// 8-15, so silu(g) * u pairs lanes lr and lr + 8 of one result.  A wave
+// loads its 16 rows whole (KH super-blocks = 1152 contiguous bytes per row
+// for n_embd 2048) into registers at once -- HBM sees each row read as one
+// burst -- and keeps
 // them while the chunk's pairs stream past in M tiles of 16: the tile's
 // Q8_K(x) rows go global -> LDS by DMA (no registers), double buffered, the
 // next tile's DMA in flight during the current tile's MFMAs.  n_embd 4096
@@ -679,12 +681,14 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
     if (ck.x < 0) return;
     const int e = ck.x, npair = ck.y, mtn = (npair + PB - 1) / PB;
     const int lane = lane_id(), wv = (int)(threadIdx.x >> 6);
-    const int lr = lane & 15, q = lane >> 4, mat = wv >> 1;
-    const int row0 = rc * GR_ROWS + 16 * (wv & 1);
+    const int lr = lane & 15, q = lane >> 4;
+    // wave w holds rows row0 .. row0 + 7 of h: lanes lr < 8 the gate rows,
+    // lanes 8-15 the same rows of up
+    const int row0 = rc * GR_ROWS + 8 * wv;
     constexpr size_t rowb = (size_t)NBE * Q4K_BYTES;
-    const uint8_t *wrow = (mat == 0 ? (e < E ? gate_exps + (size_t)e * F * rowb : gate_sh)
-                                    : (e < E ? up_exps + (size_t)e * F * rowb : up_sh)) +
-                          (size_t)(row0 + lr) * rowb;
+    const uint8_t *wrow = (lr < 8 ? (e < E ? gate_exps + (size_t)e * F * rowb : gate_sh)
+                                  : (e < E ? up_exps + (size_t)e * F * rowb : up_sh)) +
+                          (size_t)(row0 + (lr & 7)) * rowb;
     // the weight rows go out first; the pair ids follow as scalar loads
     // (their own counter), so waiting for them leaves the weights in flight
     Q4V<KH> w;
@@ -735,32 +739,17 @@ __global__ __launch_bounds__(256, 2) void gateup_rows_kernel(
                 }
             }
         }
-        __syncthreads();                       // the buffers are free for the next pass / the hand-off
+        if (ps + 1 < NPASS) __syncthreads();   // the buffers are free for the next pass
     }
-    // h = silu(g) * u: the up waves hand their sums to the gate waves
-    // through LDS
-    float *ex = (float *)s_aq0;
-    auto exi = [&](int m, int i) { return (((wv & 1) * (MC / PB) + m) * 4 + i) * 64 + lane; };
-    if (mat == 1) {
+    // h = silu(g) * u: gate lane lr and up lane lr + 8 of one result (row_ror:8)
 #pragma unroll
-        for (int m = 0; m < MC / PB; m++)
+    for (int m = 0; m < MC / PB; m++)
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (m < mtn) ex[exi(m, i)] = r[m][i];
-    }
-    __syncthreads();
-    if (mat == 0) {
-#pragma unroll
-        for (int m = 0; m < MC / PB; m++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int pr = s_pair[PB * m + 4 * q + i];
-                if (m < mtn && pr >= 0) {
-                    const float g = r[m][i], uu = ex[exi(m, i)];
-                    h[(size_t)pr * F + row0 + lr] = (g / (1.0f + expf(-g))) * uu;
-                }
-            }
-    }
+        for (int i = 0; i < 4; i++) {
+            const float g = r[m][i], uu = dpp_f<0x128>(r[m][i]);
+            const int pr = s_pair[PB * m + 4 * q + i];
+            if (lr < 8 && m < mtn && pr >= 0) h[(size_t)pr * F + row0 + lr] = (g / (1.0f + expf(-g))) * uu;
+        }
 }
 
 // ----------------------------------------------------------------- down --
