@@ -8,14 +8,16 @@
 //                        expert is bucket E with one pair per token
 //   gateup_rows_kernel   h = silu(x.G) * (x.U) per pair: chunks of up to 64
 //                        pairs of one expert x 32 rows of h, the weight rows
-//                        resident in registers; the 6-bit sub-block scales
-//                        folded into the weight operand (sc = 8 sh + sl), two
-//                        v_mfma_i32_16x16x64_i8 chains per 16 pairs x 16 rows
-//                        x 64 k, the min term on the fp32 MFMA
+//                        resident in registers (16-byte pieces per lane); the
+//                        6-bit sub-block scales folded into the weight operand
+//                        (sc = 8 sh + sl), two v_mfma_i32_16x16x64_i8 chains
+//                        per 16 pairs x 16 rows (8 gate, 8 up) x 64 k, the min
+//                        term on the fp32 MFMA
 //   q8k_quant_kernel     Q8_K(h) per pair
 //   down_rows_kernel     y[pair] = Q8_K(h) . D^T per chunk x 64 rows: Q6_K
-//                        per 16-wide group (the MFMA's other 16 k are zero)
-//                        or Q4_K per sub-block
+//                        one 16-value group per MFMA result (the activations
+//                        of the other three lane quarters zero), or Q4_K per
+//                        sub-block
 //   combine_kernel       out[t] = sum_k w_k y[t,k] + gs y[t,shared] in the
 //                        reference order (nn.c:614-629), plus an optional
 //                        residual
@@ -25,10 +27,10 @@
 // sub-block scales folded in (gate/up: sum_j sc_j P_j = sum(q sl) + 8
 // sum(q sh), every operand byte <= 105) -- the integer sums of src/q8k.c;
 // where the scale products are formed after the MFMA they are accumulated
-// exactly in int32 per super-block (with 24-bit
-// multiplies, exact here: |MFMA result| <= 32*15*128 < 2^17 and the
-// scales are 6- or 8-bit; v_mad_i32_i24 runs at the full VALU rate where a
-// 32-bit multiply takes four passes); only the
+// exactly in int32 per super-block (with 24-bit multiplies, exact here:
+// |MFMA result| <= 32*15*128 < 2^17 for a Q4_K sub-block, 16*32*128 for a
+// Q6_K group, and the scales are 6- or 8-bit; v_mad_i32_i24 runs at the full
+// VALU rate where a 32-bit multiply takes four passes); only the
 // fp32 epilogue (scale * xd * integer sum) is associated differently from
 // the reference's per-sub-block fp32 terms, well inside 1e-4 of max|y|.
 //
