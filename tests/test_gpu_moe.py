@@ -345,6 +345,23 @@ def test_moe_grouped_repeatable(qm):
     rl.close()
 
 
+def test_moe_prefill_large_ragged_batch(qm, orc):
+    """A batch three times C5's and not a multiple of the 64-token router
+    tile (T = 1500: 12,000 routed pairs, about 400 chunks, a partial router
+    tile row), against the oracle: every token's output (stage 3), the router
+    and h of every 50th token."""
+    rl = qm.ResidentLayer(seed=58, layer=0, router_bias_std=1.0)
+    hl = host_of(orc, rl)
+    T = 1500
+    x = orc.fill_normal(1500, T * 2048, 0.0, 1.0)
+    orc.set_threads(8)
+    try:
+        check_layer_staged(qm, orc, rl, hl, x, T, stage1_tokens=range(0, T, 50))
+    finally:
+        orc.set_threads(1)
+    rl.close()
+
+
 def test_moe_stack_small(qm, orc):
     cfg = dict(n_embd=512, n_ff=256, n_expert=16, n_used=4)
     hls = [make_host_layer(orc, seed=60 + i, **cfg) for i in range(4)]
