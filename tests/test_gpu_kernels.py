@@ -107,7 +107,9 @@ def test_q6k_integer_path_exact(qm, orc):
 @pytest.mark.parametrize("wtype", [12, 14])
 @pytest.mark.parametrize("n_in,n_out,T", [(256, 1, 1), (512, 2048, 1), (2048, 2048, 1),
                                           (2048, 37, 1), (4096, 300, 1), (8192, 65, 1),
-                                          (2048, 129, 4), (512, 513, 3)])
+                                          (2048, 129, 4), (512, 513, 3),
+                                          # the engine's projection shapes (qma.h:196-199): wq, wk/wv, wo
+                                          (2048, 8192, 1), (2048, 512, 1), (4096, 2048, 1)])
 def test_matvec_vs_oracle(qm, orc, wtype, n_in, n_out, T):
     W = orc.quantize(orc.fill_normal(1000 + n_in + n_out, n_in * n_out, 0.0, 0.02), wtype)
     x = orc.fill_normal(7 + T, n_in * T, 0.0, 1.0)
