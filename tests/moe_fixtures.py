@@ -8,8 +8,9 @@ def tensor_seed(seed: int, tag: int) -> int:
 
 
 def make_host_layer(orc, seed, n_embd=2048, n_ff=512, n_expert=256, n_used=8,
-                    t_down=14, zero_router=False, router_bias_std=None):
+                    t_down=14, zero_router=False, router_bias_std=None, t_down_sh=None):
     N, F, E = n_embd, n_ff, n_expert
+    t_down_sh = t_down if t_down_sh is None else t_down_sh
     if zero_router:
         gate_inp = np.zeros(E * N, np.float32)
     else:
@@ -20,9 +21,9 @@ def make_host_layer(orc, seed, n_embd=2048, n_ff=512, n_expert=256, n_used=8,
     wsh = orc.fill_normal(tensor_seed(seed, 5), N, 0.0, 0.02)
     gate_sh = orc.quantize_q4k(orc.fill_normal(tensor_seed(seed, 6), F * N, 0.0, 0.02))
     up_sh = orc.quantize_q4k(orc.fill_normal(tensor_seed(seed, 7), F * N, 0.0, 0.02))
-    down_sh = orc.quantize(orc.fill_normal(tensor_seed(seed, 8), N * F, 0.0, 0.02), t_down)
+    down_sh = orc.quantize(orc.fill_normal(tensor_seed(seed, 8), N * F, 0.0, 0.02), t_down_sh)
     bias = None
     if router_bias_std is not None:
         bias = orc.fill_normal(tensor_seed(seed, 9), E, 0.0, router_bias_std)
     return orc.HostLayer(N, F, E, n_used, gate_inp, gate_exps, up_exps, down_exps, t_down,
-                         wsh, gate_sh, up_sh, down_sh, t_down, router_bias=bias)
+                         wsh, gate_sh, up_sh, down_sh, t_down_sh, router_bias=bias)

@@ -362,6 +362,22 @@ def test_moe_prefill_large_ragged_batch(qm, orc):
     rl.close()
 
 
+@pytest.mark.parametrize("t_down,t_down_sh", [(14, 12), (12, 14)])
+def test_moe_layer_mixed_down_types(qm, orc, t_down, t_down_sh):
+    """The shared expert's down tensor in another type than the routed ones
+    (GGUF files mix Q4_K and Q6_K per tensor): one token (the fused decode
+    takes only one down type, so this runs the launch sequence), 3 tokens
+    (the launch sequence) and 37 (the grouped prefill, whose down kernel picks
+    the type per bucket), against the oracle."""
+    hl = make_host_layer(orc, seed=71, n_embd=2048, n_ff=512, n_expert=32, n_used=8, t_down=t_down,
+                         t_down_sh=t_down_sh)
+    rl = qm.ResidentLayer.from_host(hl)
+    for T in (1, 3, 37):
+        x = orc.fill_normal(900 + T, T * 2048, 0.0, 1.0)
+        check_layer_staged(qm, orc, rl, hl, x, T)
+    rl.close()
+
+
 def test_moe_stack_small(qm, orc):
     cfg = dict(n_embd=512, n_ff=256, n_expert=16, n_used=4)
     hls = [make_host_layer(orc, seed=60 + i, **cfg) for i in range(4)]
