@@ -233,7 +233,10 @@ int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *out, int T)
 
 /* Decode over a stack of MoE layers: for each of n_tok tokens in turn,
    x[t] <- x[t] + moe_l(x[t]) for l = 0..n_layer-1 (the residual add of
-   qma_eval, nn.c:2252).  x: f32 [n_tok][n_embd], updated in place. */
+   qma_eval, nn.c:2252).  x: f32 [n_tok][n_embd], updated in place.  Layers
+   may differ in down type (Q4_K/Q6_K per tensor, as GGUF quant mixes have
+   them): the persistent decode kernel takes each run of consecutive layers
+   it can, the launch sequence the others. */
 int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, float *x, int n_tok);
 
 /* Stage outputs of the last qmag_moe_ffn_dev / qmag_moe_stack_dev layer

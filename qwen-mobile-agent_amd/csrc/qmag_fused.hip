@@ -952,6 +952,7 @@ struct FusedCall {
     std::vector<qmag_moe_layer> layers;
     float *x = nullptr, *out = nullptr;   // out == nullptr: the stack (x updated in place)
     int n_tok = 0;
+    int lpt = 1;                          // persistent launches per token (fused runs of a mixed stack)
     unsigned first_epoch = 0;             // epoch of the call's first launch (token 0)
     int snap = -1;                        // snapshot slot holding the input rows, or -1
 };
@@ -969,8 +970,8 @@ static int replay(const std::vector<FusedCall> &log, unsigned e, hipStream_t s)
 {
     const size_t N = fused::N;
     for (const FusedCall &c : log) {
-        if (c.first_epoch + (unsigned)c.n_tok <= e) continue;         // finished before launch e
-        const int t0 = e > c.first_epoch ? (int)(e - c.first_epoch) : 0;
+        if (c.first_epoch + (unsigned)(c.n_tok * c.lpt) <= e) continue;   // finished before launch e
+        const int t0 = e > c.first_epoch ? (int)((e - c.first_epoch) / (unsigned)c.lpt) : 0;
         const size_t rows = (size_t)(c.n_tok - t0) * N;
         if (c.snap >= 0)
             QMAG_HIP(hipMemcpyAsync(c.x + t0 * N, g_snap[c.snap] + t0 * N, sizeof(float) * rows,
@@ -1168,6 +1169,82 @@ int fused_call(const qmag_moe_layer *L, int n_layer, float *x, float *out, int n
     for (int t = 0; t < n_tok; t++) {
         st = fused_launch(L, dl, n_layer, x + (size_t)t * fused::N, out ? out + (size_t)t * fused::N : nullptr, s);
         if (st) return st;
+    }
+    return QMAG_OK;
+}
+
+// A stack the persistent kernel cannot take whole (down types that change
+// from layer to layer, a shared expert typed apart from the routed ones):
+// the maximal runs of consecutive layers it can take go through it, the other
+// layers through the launch sequence, token by token in layer order.  The
+// whole stack's descriptors are uploaded once and each run reads its slice.
+// One log entry and one input snapshot per token cover the token's launches,
+// so an expired wait replays the token's whole stack through the launch
+// sequence.  Returns 1 (nothing launched) when no layer qualifies.
+int fused_stack_runs(const qmag_moe_layer *L, int n_layer, float *x, int n_tok, hipStream_t s)
+{
+    if (n_layer < 2 || n_layer > 256) return 1;
+    std::vector<int> rb, re;
+    std::vector<char> rf;
+    for (int b = 0; b < n_layer;) {
+        int e = b + 1;
+        const bool f = fused_eligible(L + b, 1);
+        if (f)
+            while (e < n_layer && fused_eligible(L + b, e + 1 - b)) e++;
+        else
+            while (e < n_layer && !fused_eligible(L + e, 1)) e++;
+        rb.push_back(b);
+        re.push_back(e);
+        rf.push_back(f);
+        b = e;
+    }
+    int nf = 0;
+    for (char f : rf) nf += f;
+    if (nf == 0) return 1;
+    const qmag_moe_layer *dl = nullptr;
+    int st = fused_prepare(L, n_layer, s, &dl);
+    if (st) return st;
+    for (int t = 0; t < n_tok; t++) {
+        float *xt = x + (size_t)t * fused::N;
+        const bool wraps = g_epoch + (unsigned)nf >= (1u << 24);
+        if (g_log.size() >= (size_t)LOG_CALLS || g_snap_used == SNAP_SLOTS || wraps) {
+            st = fused_status();
+            if (st) return st;
+            if (wraps) {
+                st = rearm();
+                if (st) return st;
+            }
+        }
+        FusedCall c;
+        c.layers.assign(L, L + n_layer);
+        c.x = xt;
+        c.n_tok = 1;
+        c.lpt = nf;
+        c.first_epoch = g_epoch;
+        const int slot = g_snap_used++;
+        const size_t need = sizeof(float) * fused::N;
+        if (need > g_snap_bytes[slot]) {
+            QMAG_HIP(hipStreamSynchronize(s));
+            if (g_snap[slot]) QMAG_HIP(hipFree(g_snap[slot]));
+            g_snap[slot] = nullptr;
+            g_snap_bytes[slot] = 0;
+            QMAG_HIP(hipMalloc(&g_snap[slot], need));
+            g_snap_bytes[slot] = need;
+        }
+        QMAG_HIP(hipMemcpyAsync(g_snap[slot], xt, need, hipMemcpyDeviceToDevice, s));
+        c.snap = slot;
+        g_log.push_back(std::move(c));
+        for (size_t r = 0; r < rb.size(); r++) {
+            if (rf[r]) {
+                st = fused_launch(L + rb[r], dl + rb[r], re[r] - rb[r], xt, nullptr, s);
+                if (st) return st;
+            } else {
+                for (int l = rb[r]; l < re[r]; l++) {
+                    st = moe_ffn(&L[l], xt, xt, 1, xt, s);
+                    if (st) return st;
+                }
+            }
+        }
     }
     return QMAG_OK;
 }

@@ -100,6 +100,9 @@ bool fused_eligible(const qmag_moe_layer *L, int n_layer);
 // n_tok tokens through n_layer layers, one launch per token: x (and out,
 // when not null: one layer, out = moe(x)) are [n_tok][2048]
 int fused_call(const qmag_moe_layer *L, int n_layer, float *x, float *out, int n_tok, hipStream_t s);
+// a stack fused_eligible refuses as a whole: its eligible runs fused, the rest
+// through the launch sequence; 1 when no layer qualifies (nothing launched)
+int fused_stack_runs(const qmag_moe_layer *L, int n_layer, float *x, int n_tok, hipStream_t s);
 long fused_recoveries();
 void fused_test_abort_next(int nth);
 // the launch sequence wrote the latest stage outputs (qmag_moe_last_stage)

@@ -600,6 +600,14 @@ extern "C" int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, flo
         g_last_fused = true;
         return fused_call(layers, n_layer, x, nullptr, n_tok, ctx().stream);
     }
+    if (option(QMAG_OPT_FUSED)) {
+        st = fused_stack_runs(layers, n_layer, x, n_tok, ctx().stream);
+        if (st != 1) {
+            // the stage buffers hold the last layer's, from whichever path ran it
+            g_last_fused = fused_eligible(&layers[n_layer - 1], 1);
+            return st;
+        }
+    }
     g_last_fused = false;
     for (int t = 0; t < n_tok; t++) {
         float *xt = x + (size_t)t * N;

@@ -585,12 +585,78 @@ def test_fused_abort_recovery_stack(qm, orc, nth):
         r.close()
 
 
+MIXED = [(14, 14), (14, 14), (12, 12), (12, 12), (14, 12), (14, 14)]   # (routed, shared) down types
+
+
+def _mixed_stack(qm, orc):
+    hls = [make_host_layer(orc, seed=80 + i, n_embd=2048, n_ff=512, n_expert=64, n_used=8, t_down=td,
+                           t_down_sh=ts) for i, (td, ts) in enumerate(MIXED)]
+    return hls, [qm.ResidentLayer.from_host(h) for h in hls]
+
+
+def test_moe_stack_mixed_down_types(qm, orc):
+    """A stack whose down types change from layer to layer (GGUF quant mixes
+    do) and with one layer whose shared expert is typed apart: the persistent
+    kernel takes the runs of layers it can (here layers 0-1, 2-3 and 5), the
+    launch sequence the rest.  Every token equals the layers applied one call
+    at a time (each through the path that takes it alone) bit for bit, and
+    each of those layers is checked against the oracle stage by stage on its
+    own input (teacher forcing: end to end, a near-tie in one layer's routing
+    may pick another expert on either side)."""
+    hls, rls = _mixed_stack(qm, orc)
+    n_tok = 3
+    x = orc.fill_normal(33, n_tok * 2048, 0.0, 1.0)
+    xb = qm.DBuf.from_array(x)
+    qm.moe_stack_dev([r.c for r in rls], xb.ptr, n_tok)
+    got = xb.download(np.float32).reshape(n_tok, 2048)
+    for t in range(n_tok):
+        xl = x[t * 2048:(t + 1) * 2048].copy()
+        for r, h in zip(rls, hls):
+            check_layer_staged(qm, orc, r, h, xl, 1)
+            b = qm.DBuf.from_array(xl)
+            qm.moe_stack_dev([r.c], b.ptr, 1)
+            xl = b.download(np.float32)
+        assert np.array_equal(got[t].view(np.uint32), xl.view(np.uint32)), f"token {t}"
+    for r in rls:
+        r.close()
+
+
+@pytest.mark.parametrize("nth", [2, 5])
+def test_fused_abort_recovery_mixed_stack(qm, orc, nth):
+    """With the nth persistent launch of a mixed stack's call aborted (3 fused
+    runs per token), the tokens before its token keep the mixed path's result
+    and the rest are restored and re-run through the launch sequence."""
+    hls, rls = _mixed_stack(qm, orc)
+    cl = [r.c for r in rls]
+    x = orc.fill_normal(14, 3 * 2048, 0.0, 1.0)
+    res = {}
+    for fused in (True, False):
+        qm.set_fused(fused)
+        xb = qm.DBuf.from_array(x)
+        qm.moe_stack_dev(cl, xb.ptr, 3)
+        res[fused] = xb.download(np.float32).reshape(3, 2048)
+    qm.set_fused(True)
+    n0 = qm.fused_recoveries()
+    qm.arm_test_abort(nth)
+    xb = qm.DBuf.from_array(x)
+    qm.moe_stack_dev(cl, xb.ptr, 3)
+    got = xb.download(np.float32).reshape(3, 2048)
+    assert qm.fused_recoveries() == n0 + 1
+    for t in range(3):
+        want = res[True][t] if t < (nth - 1) // 3 else res[False][t]
+        assert np.array_equal(got[t].view(np.uint32), want.view(np.uint32)), f"token {t}"
+    for r in rls:
+        r.close()
+
+
 @pytest.mark.parametrize("n_used", [1, 2, 3])
 def test_stack_small_n_used(qm, orc, n_used):
     """Multi-layer decode with fewer than 4 routed experts per token (not
-    eligible for the single persistent launch, whose one-slot hand-offs need
-    every workgroup on each layer's dependency chain): 4 layers, against the
-    oracle's residual chain."""
+    eligible for a multi-layer persistent launch, whose one-slot hand-offs
+    need every workgroup on each layer's dependency chain, so every layer
+    runs as its own one-layer launch): 4 layers.  The stack equals its layers
+    chained one call at a time bit for bit, and each layer is checked against
+    the oracle stage by stage on the GPU's own x_l."""
     hls = [make_host_layer(orc, seed=70 + i, n_embd=2048, n_ff=512, n_expert=32, n_used=n_used)
            for i in range(4)]
     rls = [qm.ResidentLayer.from_host(h) for h in hls]
@@ -598,18 +664,14 @@ def test_stack_small_n_used(qm, orc, n_used):
     xb = qm.DBuf.from_array(x)
     qm.moe_stack_dev([r.c for r in rls], xb.ptr, 2)
     got = xb.download(np.float32).reshape(2, 2048)
-    qm.set_fused(False)         # one-layer calls through the same kernels as the stack
-    try:
-        for t in range(2):
-            # the stack equals its layers chained one call at a time, bit for bit
-            xl = x[t * 2048:(t + 1) * 2048].copy()
-            for l in range(4):
-                # each layer stage by stage against the oracle on the GPU's own x_l
-                y = check_layer_staged(qm, orc, rls[l], hls[l], xl, 1)[0]
-                xl = (xl + y).astype(np.float32)
-            assert np.array_equal(got[t].view(np.uint32), xl.view(np.uint32)), f"token {t}"
-    finally:
-        qm.set_fused(True)
+    for t in range(2):
+        xl = x[t * 2048:(t + 1) * 2048].copy()
+        for l in range(4):
+            check_layer_staged(qm, orc, rls[l], hls[l], xl, 1)
+            b = qm.DBuf.from_array(xl)
+            qm.moe_stack_dev([rls[l].c], b.ptr, 1)
+            xl = b.download(np.float32)
+        assert np.array_equal(got[t].view(np.uint32), xl.view(np.uint32)), f"token {t}"
     for r in rls:
         r.close()
 
