@@ -46,24 +46,20 @@ def test_gguf_moe_layers_vs_oracle(qm, orc, model):
                 check_layer(qm, orc, rl, hl, x, T)
             x = orc.fill_normal(60 + il, 16 * N, 0.0, 1.0)
             check_layer_staged(qm, orc, rl, hl, x, 16)        # grouped prefill
-        # the stack over both layers (down types differ: the launch sequence)
-        # equals the layers chained one call at a time, bit for bit
+        # the stack over both layers (down types differ: each layer is its own
+        # one-layer persistent launch) equals the layers chained one call at a
+        # time, bit for bit
         x = orc.fill_normal(77, 2 * N, 0.0, 1.0)
         xb = qm.DBuf.from_array(x)
         qm.moe_stack_dev(dev, xb.ptr, 2)
         got = xb.download(np.float32).reshape(2, N)
-        qm.set_fused(False)
-        try:
-            for t in range(2):
-                xl = x[t * N:(t + 1) * N].copy()
-                for L in dev:
-                    xin = qm.DBuf.from_array(xl)
-                    out = qm.DBuf(4 * N)
-                    qm.moe_ffn_dev(L, xin.ptr, out.ptr, 1)
-                    xl = (xl + out.download(np.float32)).astype(np.float32)
-                assert np.array_equal(got[t].view(np.uint32), xl.view(np.uint32))
-        finally:
-            qm.set_fused(True)
+        for t in range(2):
+            xl = x[t * N:(t + 1) * N].copy()
+            for L in dev:
+                b = qm.DBuf.from_array(xl)
+                qm.moe_stack_dev([L], b.ptr, 1)
+                xl = b.download(np.float32)
+            assert np.array_equal(got[t].view(np.uint32), xl.view(np.uint32)), f"token {t}"
     finally:
         for L in dev:
             qm.Gguf.free_moe_layer(L)
