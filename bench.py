@@ -138,16 +138,24 @@ def matvec_bytes(n_in: int, n_out: int, wtype: int) -> int:
 
 
 def aux_matvec(name: str, n_in: int, n_out: int, wtype: int, copies: int, seconds: float,
-               cpu_seconds: float) -> dict:
+               cpu_seconds: float, repack: bool = False) -> dict:
     """Configs C1/C2: the matmul seam at T = 1 (one launch: the matvec
     quantises x to Q8_K itself), rotating over `copies` distinct weight
     matrices so the working set exceeds the 256 MB last-level cache; the CPU
     baseline is the oracle's matmul (mm_worker rows over min(nproc, 16)
-    pool threads, nn.c:276-303) on the first copy's bytes."""
+    pool threads, nn.c:276-303) on the first copy's bytes.  With `repack`
+    the Q6_K matrices are repacked once (qmag_repack_q6k_dev, outside the
+    timed region) and timed as QMAG_TYPE_Q6_K_R: the same bytes and results."""
     rb = n_in // 256 * (144 if wtype == 12 else 210)
     Ws = [qmag.DBuf(rb * n_out) for _ in range(copies)]
     for i, w in enumerate(Ws):
         qmag.synth_weights(0xC100 + i, n_in * n_out, 0.02, wtype, w.ptr)
+    if repack:
+        Rs = [qmag.DBuf(rb * n_out) for _ in range(copies)]
+        for w, r in zip(Ws, Rs):
+            qmag.repack_q6k_dev(w, r, n_in, n_out)
+            w.close()
+        Ws, wtype = Rs, qmag.TYPE_Q6_K_R
     x = qmag.DBuf(4 * n_in)
     qmag.synth_normal(0xC1, n_in, 0.0, 1.0, x.ptr)
     out = qmag.DBuf(4 * n_out)
@@ -496,8 +504,10 @@ def main() -> int:
         legs = {
             "c1": lambda: aux_matvec("C1: Q4_K matvec 2048x2048, matmul seam, T=1", 2048, 2048, 12, 128,
                                      args.aux_seconds, cs),
-            "c2": lambda: aux_matvec("C2: Q6_K LM head 151936x2048, matmul seam, T=1", 2048, 151936, 14, 2,
-                                     args.aux_seconds, cs),
+            "c2": lambda: {**aux_matvec("C2: Q6_K LM head 151936x2048, matmul seam, T=1", 2048, 151936, 14, 2,
+                                        args.aux_seconds, cs),
+                           "repacked": aux_matvec("C2 repacked: the same Q6_K LM head as QMAG_TYPE_Q6_K_R rows",
+                                                  2048, 151936, 14, 2, args.aux_seconds, 0.0, repack=True)},
             "c3": lambda: aux_layer(cl, args.aux_seconds, cpu["us_per_layer_token"] if cpu else None),
             "c5": lambda: aux_prefill(args.aux_seconds, cs),
             "projections": lambda: aux_projections(args.aux_seconds / 4),

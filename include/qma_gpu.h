@@ -34,6 +34,10 @@ extern "C" {
 
 #define QMAG_TYPE_Q4_K 12
 #define QMAG_TYPE_Q6_K 14
+/* Q6_K rows repacked by qmag_repack_q6k_dev for the matmul entries (a layout
+   of this library with no counterpart in the reference or the GGUF; the same
+   bytes per row, the same results as QMAG_TYPE_Q6_K). */
+#define QMAG_TYPE_Q6_K_R 270
 
 #define QMAG_OK 0
 #define QMAG_ERR_HIP (-1)      /* a HIP runtime call failed                  */
@@ -179,6 +183,19 @@ int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum,
    quantises x itself, bit-identically).  n_in: any multiple of 256. */
 int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
                     float *out);
+
+/* Repack n_out Q6_K rows of n_in weights (n_in a multiple of 2048) from the
+   block layout (block_q6_K, qma.h; what the GGUF holds) into the row layout
+   the matmul entries read fastest, for wtype QMAG_TYPE_Q6_K_R: per row, each
+   super-block's 16-byte low ql task pieces, then the high ones, then the qh
+   bytes, the scales and the d values of every super-block (n_out * n_in / 256
+   * 210 bytes, as before).  No counterpart in the reference: a one-time
+   transform at weight upload for large Q6_K matrices such as the LM head
+   (nn.c:2243).  dst: device memory of the same size, 16-byte aligned, not
+   overlapping src.  Results of qmag_matmul_dev / qmag_matmul_q8k_dev /
+   qmag_matmul_noalloc_dev on the repacked rows are bit-identical to those on
+   the block layout. */
+int qmag_repack_q6k_dev(const void *src, void *dst, int n_in, int n_out);
 
 /* The matmul seam without any allocation (no counterpart in the reference):
    for callers that cannot allocate -- code under HIP graph capture, serving

@@ -78,6 +78,7 @@ int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const 
 // T = 1 with x in f32: the matvec quantises x to Q8_K itself (bit-identical);
 // available for the row lengths matvec_x_supported() accepts
 bool matvec_x_supported(int n_in);
+int launch_repack_q6k(const void *src, void *dst, int n_in, int n_out, hipStream_t s);
 int launch_matvec_x(const float *x, const void *W, int n_in, int n_out, int wtype, float *out, hipStream_t s);
 // fp32 path of quants.c (qmag_quants.hip)
 int launch_dequant(const void *W, int wtype, long n, float *y, hipStream_t s);

@@ -16,7 +16,7 @@
 #define QMAG_MV_U 2
 #endif
 #ifndef QMAG_MV_CAP
-#define QMAG_MV_CAP 32
+#define QMAG_MV_CAP 64
 #endif
 #ifndef QMAG_MV_WG
 #define QMAG_MV_WG 256
@@ -63,8 +63,10 @@ struct RowTask<QMAG_TYPE_Q4_K> {
     };
     using Act = Q4Act;
     static constexpr int BLOCK = Q4K_BYTES;
-    __device__ static void load_raw(Raw &r, const uint8_t *blk, int q)
+    // task q of super-block ib of the row at rowp (nb super-blocks)
+    __device__ static void load_raw(Raw &r, const uint8_t *rowp, int ib, int q, int)
     {
+        const uint8_t *blk = rowp + (size_t)ib * BLOCK;
         r.hdr = ld16(blk);
         r.q0 = ld16(blk + 16 + 32 * q);
         r.q1 = ld16(blk + 32 + 32 * q);
@@ -89,9 +91,9 @@ struct RowTask<QMAG_TYPE_Q6_K> {
         float xd;
     };
     static constexpr int BLOCK = Q6K_BYTES;
-    __device__ static void load_raw(Raw &r, const uint8_t *blk, int q)
+    __device__ static void load_raw(Raw &r, const uint8_t *rowp, int ib, int q, int)
     {
-        q6_load_raw(r, blk, q >> 1, q & 1);
+        q6_load_raw(r, rowp + (size_t)ib * BLOCK, q >> 1, q & 1);
     }
     __device__ static void load_act(Act &a, const int8_t *xq, const float *xd, const int16_t *,
                                     int ib, int q)
@@ -107,6 +109,64 @@ struct RowTask<QMAG_TYPE_Q6_K> {
         return q == 0 ? h2f(r.d) * a.xd * (float)isum : 0.0f;
     }
 };
+
+// Q6_K rows repacked for the matvec (QMAG_TYPE_Q6_K_R; a layout of this
+// library, not of the GGUF): a row of nb super-blocks, nb a multiple of 8 so
+// every row starts on 16 bytes, is stored as planes -- each block's four
+// 16-byte low ql task pieces (ql[0,16), [16,32), [64,80), [80,96)), then
+// every block's four high ones ([32,48), [48,64), [96,112), [112,128)), then
+// the qh bytes, the scales and the d values of every block, nb * 210 bytes
+// as before.  A task's loads are then aligned and the row's lanes read 512
+// contiguous bytes per ql or qh load; the bytes a task holds, and so its dot,
+// are those of the block layout.
+template <>
+struct RowTask<QMAG_TYPE_Q6_K_R> : RowTask<QMAG_TYPE_Q6_K> {
+    __device__ static void load_raw(Raw &r, const uint8_t *rowp, int ib, int q, int nb)
+    {
+        r.ql_lo = ld16(rowp + 64 * ib + 16 * q);
+        r.ql_hi = ld16(rowp + 64 * (nb + ib) + 16 * q);
+        r.qh = ld16(rowp + 64 * (2 * nb + ib) + 16 * q);
+        r.sc = ld8(rowp + 192 * nb + 16 * ib + 8 * (q >> 1));
+        r.d = ld2(rowp + 208 * nb + 2 * ib);
+    }
+};
+
+// Block layout -> repacked rows: one thread per super-block.
+__global__ __launch_bounds__(256) void repack_q6k_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                         int nb, long nblocks)
+{
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nblocks) return;
+    const long row = i / nb;
+    const int ib = (int)(i % nb);
+    const uint8_t *b = src + i * Q6K_BYTES;
+    uint8_t *rp = dst + row * nb * Q6K_BYTES;
+    for (int q = 0; q < 4; q++)
+        for (int j = 0; j < 16; j++) {
+            rp[64 * ib + 16 * q + j] = b[64 * (q >> 1) + 16 * (q & 1) + j];
+            rp[64 * (nb + ib) + 16 * q + j] = b[64 * (q >> 1) + 32 + 16 * (q & 1) + j];
+        }
+    for (int j = 0; j < 64; j++) rp[64 * (2 * nb + ib) + j] = b[128 + j];
+    for (int j = 0; j < 16; j++) rp[192 * nb + 16 * ib + j] = b[192 + j];
+    rp[208 * nb + 2 * ib] = b[208];
+    rp[208 * nb + 2 * ib + 1] = b[209];
+}
+
+int launch_repack_q6k(const void *src, void *dst, int n_in, int n_out, hipStream_t s)
+{
+    if (n_in <= 0 || n_in % (8 * QK_K) || n_out <= 0)
+        return fail(QMAG_ERR_ARG, "repack_q6k: n_in=%d (a multiple of 2048) n_out=%d", n_in, n_out);
+    if (!src || !dst || ((uintptr_t)dst & 15))
+        return fail(QMAG_ERR_ARG, "repack_q6k: null or unaligned pointer (dst needs 16-byte alignment)");
+    const size_t bytes = (size_t)n_out * (n_in / QK_K) * Q6K_BYTES;
+    const uintptr_t a = (uintptr_t)src, b = (uintptr_t)dst;
+    if (a < b + bytes && b < a + bytes) return fail(QMAG_ERR_ARG, "repack_q6k: src and dst overlap");
+    const long nblocks = (long)n_out * (n_in / QK_K);
+    hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, s,
+                       (const uint8_t *)src, (uint8_t *)dst, n_in / QK_K, nblocks);
+    QMAG_HIP(hipGetLastError());
+    return QMAG_OK;
+}
 
 // ONE_TOKEN: T = 1, the activation operand is loaded once per lane.  XF
 // (with ONE_TOKEN): the kernel takes x itself and every workgroup computes
@@ -144,7 +204,7 @@ __global__ __launch_bounds__(QMAG_MV_WG) void matvec_kernel(const uint8_t *__res
 #pragma unroll
             for (int j = 0; j < TPL; j++) {
                 if (row < n_out)
-                    RT::load_raw(raw[u][j], W + (size_t)row * RB + (size_t)((sub + LPR * j) >> 2) * RT::BLOCK, q);
+                    RT::load_raw(raw[u][j], W + (size_t)row * RB, (sub + LPR * j) >> 2, q, NB);
                 else
                     raw[u][j] = typename RT::Raw{};
             }
@@ -244,7 +304,7 @@ __global__ __launch_bounds__(256) void matvec_any_kernel(const uint8_t *__restri
             for (int tk = lane; tk < ntask; tk += 64) {
                 typename RT::Raw r;
                 typename RT::Act a;
-                RT::load_raw(r, W + (size_t)row * rb + (size_t)(tk >> 2) * RT::BLOCK, q);
+                RT::load_raw(r, W + (size_t)row * rb, tk >> 2, q, nb);
                 RT::load_act(a, xq + (size_t)t * n_in, xd + (size_t)t * nb, xsum + (size_t)t * (n_in / 16),
                              tk >> 2, q);
                 v += RT::dot(r, a, q);
@@ -301,6 +361,11 @@ int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const 
         return fail(QMAG_ERR_ARG, "matvec: null pointer");
     if (wtype == QMAG_TYPE_Q4_K) return launch_mv_t<QMAG_TYPE_Q4_K>(xq, xd, xsum, W, n_in, n_out, T, out, s, nullptr);
     if (wtype == QMAG_TYPE_Q6_K) return launch_mv_t<QMAG_TYPE_Q6_K>(xq, xd, xsum, W, n_in, n_out, T, out, s, nullptr);
+    if (wtype == QMAG_TYPE_Q6_K_R) {
+        if (n_in % (8 * QK_K) || ((uintptr_t)W & 15))
+            return fail(QMAG_ERR_ARG, "matvec: repacked Q6_K needs n_in %% 2048 == 0 and 16-byte aligned rows");
+        return launch_mv_t<QMAG_TYPE_Q6_K_R>(xq, xd, xsum, W, n_in, n_out, T, out, s, nullptr);
+    }
     return fail(QMAG_ERR_ARG, "matvec: unsupported wtype %d", wtype);
 }
 
@@ -315,6 +380,11 @@ int launch_matvec_x(const float *x, const void *W, int n_in, int n_out, int wtyp
         return launch_mv_t<QMAG_TYPE_Q4_K>(nullptr, nullptr, nullptr, W, n_in, n_out, 1, out, s, x);
     if (wtype == QMAG_TYPE_Q6_K)
         return launch_mv_t<QMAG_TYPE_Q6_K>(nullptr, nullptr, nullptr, W, n_in, n_out, 1, out, s, x);
+    if (wtype == QMAG_TYPE_Q6_K_R) {
+        if (n_in % (8 * QK_K) || ((uintptr_t)W & 15))
+            return fail(QMAG_ERR_ARG, "matvec: repacked Q6_K needs n_in %% 2048 == 0 and 16-byte aligned rows");
+        return launch_mv_t<QMAG_TYPE_Q6_K_R>(nullptr, nullptr, nullptr, W, n_in, n_out, 1, out, s, x);
+    }
     return fail(QMAG_ERR_ARG, "matvec: unsupported wtype %d", wtype);
 }
 

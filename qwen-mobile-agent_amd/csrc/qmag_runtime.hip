@@ -359,6 +359,13 @@ int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum, 
     return launch_matvec(xq, xd, xsum, W, n_in, n_out, T, wtype, out, g_ctx.stream);
 }
 
+int qmag_repack_q6k_dev(const void *src, void *dst, int n_in, int n_out)
+{
+    int st = require_ready();
+    if (st) return st;
+    return launch_repack_q6k(src, dst, n_in, n_out, g_ctx.stream);
+}
+
 int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype, float *out)
 {
     int st = require_ready();

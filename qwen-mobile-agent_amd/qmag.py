@@ -18,7 +18,8 @@ LIB_PATH = os.path.join(HERE, "libqmagpu.so")
 QK_K = 256
 TYPE_Q4_K = 12
 TYPE_Q6_K = 14
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210}
+TYPE_Q6_K_R = 270          # Q6_K rows repacked by qmag_repack_q6k_dev (same bytes per row)
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q6_K_R: 210}
 
 P = C.c_void_p
 
@@ -52,6 +53,7 @@ SIGNATURES = {
     "qmag_q8k_quant_dev": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
     "qmag_matmul_q8k_dev": (C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_matmul_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+    "qmag_repack_q6k_dev": (C.c_int, [P, P, C.c_int, C.c_int]),
     "qmag_matmul_noalloc_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_dequant_dev": (C.c_int, [P, C.c_int, C.c_int64, P]),
     "qmag_matmul_f32_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
@@ -266,6 +268,10 @@ def matmul_q8k_dev(xq, xd, xs, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> Non
 
 def matmul_dev(x: DBuf, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> None:
     check(lib().qmag_matmul_dev(x.ptr, W.ptr, n_in, n_out, T, wtype, out.ptr))
+
+
+def repack_q6k_dev(src: DBuf, dst: DBuf, n_in: int, n_out: int) -> None:
+    check(lib().qmag_repack_q6k_dev(src.ptr, dst.ptr, n_in, n_out))
 
 
 def dequant_dev(W: DBuf, wtype: int, n: int, y: DBuf) -> None:

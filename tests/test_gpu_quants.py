@@ -11,7 +11,10 @@ oracle on the same bytes:
 * the matmul seam at the engine's other projection shapes (qma.h:186-199:
   wq / wqkv 2048 -> 8192, attn_gate 2048 -> 4096, wk / wv 2048 -> 512,
   ssm_beta / ssm_alpha 2048 -> 32, wo / ssm_out 4096 -> 2048; the types of
-  wv and wqkv vary).
+  wv and wqkv vary);
+* Q6_K rows repacked by qmag_repack_q6k_dev (a layout of this library):
+  bit-identical matmul results to the block layout through every matmul
+  entry, the oracle's within 1e-4, and the documented byte order.
 """
 import ctypes as C
 import threading
@@ -232,3 +235,79 @@ def test_matmul_projection_shapes(qm, orc, name, n_in, n_out, wtype):
         for t in range(T):
             assert max_rel_err(got[t], ref[t]) < TOL, (name, T, t)
     orc.set_threads(1)
+
+
+def _repack_layout(W, n_in, n_out):
+    """The row layout qmag_repack_q6k_dev documents (include/qma_gpu.h), from
+    the block bytes: per row, every super-block's low ql task pieces, then the
+    high ones, then the qh bytes, scales and d of every super-block."""
+    nb = n_in // 256
+    B = W.reshape(n_out, nb, 210)
+    ql, qh, sc, d = B[:, :, :128], B[:, :, 128:192], B[:, :, 192:208], B[:, :, 208:210]
+    lo = np.concatenate([ql[:, :, 0:32], ql[:, :, 64:96]], axis=2)
+    hi = np.concatenate([ql[:, :, 32:64], ql[:, :, 96:128]], axis=2)
+    return np.concatenate([x.reshape(n_out, -1) for x in (lo, hi, qh, sc, d)], axis=1).reshape(-1)
+
+
+@pytest.mark.parametrize("n_in,n_out", [(2048, 1000), (4096, 777), (6144, 300)])
+def test_q6k_repacked_rows_match_block_layout(qm, orc, n_in, n_out):
+    """Q6_K rows repacked for the matvec (QMAG_TYPE_Q6_K_R) give the block
+    layout's results bit for bit through every matmul entry (one-launch
+    T = 1, two-step T = 3, pre-quantised, allocation-free; n_in = 6144 runs
+    the one-wave-per-row kernel), and the oracle's within 1e-4; the
+    repacked bytes follow the documented plane order."""
+    W = orc.quantize(orc.fill_normal(7000 + n_in, n_in * n_out, 0.0, 0.02), 14)
+    Wb = qm.DBuf.from_array(W)
+    Rb = qm.DBuf(W.nbytes)
+    qm.repack_q6k_dev(Wb, Rb, n_in, n_out)
+    assert np.array_equal(Rb.download(np.uint8), _repack_layout(W, n_in, n_out))
+    L = qm.lib()
+    for T in (1, 3):
+        x = orc.fill_normal(7100 + T, T * n_in, 0.0, 1.0)
+        xb = qm.DBuf.from_array(x)
+        a, b, c = (qm.DBuf(4 * T * n_out) for _ in range(3))
+        qm.matmul_dev(xb, Wb, n_in, n_out, T, qm.TYPE_Q6_K, a)
+        qm.matmul_dev(xb, Rb, n_in, n_out, T, qm.TYPE_Q6_K_R, b)
+        qm.check(L.qmag_matmul_noalloc_dev(xb.ptr, Rb.ptr, n_in, n_out, T, qm.TYPE_Q6_K_R, c.ptr))
+        ga = a.download(np.float32)
+        assert np.array_equal(ga.view(np.uint32), b.download(np.uint32)), T
+        assert np.array_equal(ga.view(np.uint32), c.download(np.uint32)), T
+        ref = orc.matmul_q8k(x, W, n_in, n_out, T, 14)
+        for t in range(T):
+            assert max_rel_err(ga.reshape(T, n_out)[t], ref[t]) < TOL
+    xq, xd, xs = orc.q8k_quant(orc.fill_normal(7200, n_in, 0.0, 1.0))
+    a, b = qm.DBuf(4 * n_out), qm.DBuf(4 * n_out)
+    args = (qm.DBuf.from_array(xq), qm.DBuf.from_array(xd), qm.DBuf.from_array(xs))
+    qm.matmul_q8k_dev(*args, Wb, n_in, n_out, 1, qm.TYPE_Q6_K, a)
+    qm.matmul_q8k_dev(*args, Rb, n_in, n_out, 1, qm.TYPE_Q6_K_R, b)
+    assert np.array_equal(a.download(np.uint32), b.download(np.uint32))
+
+
+def test_q6k_repacked_lm_head_shape(qm, orc):
+    """The C2 shape (151,936 x 2048) repacked: bit-identical to the block
+    layout's output."""
+    n_in, n_out = 2048, 151936
+    Wb = qm.DBuf(n_in // 256 * 210 * n_out)
+    qm.synth_weights(42, n_in * n_out, 0.02, 14, Wb.ptr)
+    Rb = qm.DBuf(Wb.nbytes)
+    qm.repack_q6k_dev(Wb, Rb, n_in, n_out)
+    xb = qm.DBuf.from_array(orc.fill_normal(3, n_in, 0.0, 1.0))
+    a, b = qm.DBuf(4 * n_out), qm.DBuf(4 * n_out)
+    qm.matmul_dev(xb, Wb, n_in, n_out, 1, qm.TYPE_Q6_K, a)
+    qm.matmul_dev(xb, Rb, n_in, n_out, 1, qm.TYPE_Q6_K_R, b)
+    assert np.array_equal(a.download(np.uint32), b.download(np.uint32))
+
+
+def test_q6k_repack_rejects_bad_arguments(qm):
+    """Row lengths that are not a multiple of 2048, unaligned or overlapping
+    buffers, and the repacked type at such lengths are argument errors."""
+    L = qm.lib()
+    W = qm.DBuf(8 * 210 * 64)
+    R = qm.DBuf(8 * 210 * 64 + 64)
+    x, out = qm.DBuf(4 * 2048), qm.DBuf(4 * 64)
+    assert L.qmag_repack_q6k_dev(W.ptr, R.ptr, 1024, 64) == -2
+    assert L.qmag_repack_q6k_dev(W.ptr, R.ptr + 8, 2048, 64) == -2
+    assert L.qmag_repack_q6k_dev(W.ptr, W.ptr, 2048, 64) == -2
+    assert L.qmag_matmul_dev(x.ptr, W.ptr, 1024, 64, 1, qm.TYPE_Q6_K_R, out.ptr) == -2
+    assert L.qmag_matmul_dev(x.ptr, R.ptr + 8, 2048, 64, 1, qm.TYPE_Q6_K_R, out.ptr) == -2
+    assert L.qmag_repack_q6k_dev(W.ptr, R.ptr, 2048, 64) == 0
