@@ -26,6 +26,8 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "qwen-mobile-agent_amd"))
 
+import ctypes as C
+
 import numpy as np  # noqa: E402
 
 import qmag  # noqa: E402
@@ -232,7 +234,60 @@ def aux_projections(seconds: float) -> dict:
         for w in Ws:
             w.close()
     log("projections: " + ", ".join(f"{k} {v['us_per_call']:.2f} us ({v['gbps']:.0f} GB/s)" for k, v in out.items()))
+    out["groups"] = aux_projection_groups(seconds)
     return out
+
+
+# projections the engine computes from one x, timed as one qmag_matmul_group_dev
+# launch against separate qmag_matmul_dev calls: q/k/v (nn.c:2111-2113) and the
+# recurrent layer's qkv, gate, beta and alpha (nn.c:2162, 2165-2170)
+PROJECTION_GROUPS = [("attn_qkv", 2048, [("wq", 8192, 12), ("wk", 512, 12), ("wv_q6k", 512, 14)]),
+                     ("ssm_in", 2048, [("wqkv_q6k", 8192, 14), ("attn_gate", 4096, 12), ("ssm_beta", 32, 12),
+                                       ("ssm_alpha", 32, 12)])]
+
+
+def aux_projection_groups(seconds: float) -> dict:
+    L = qmag.lib()
+    res = {}
+    for gname, n_in, mats in PROJECTION_GROUPS:
+        rbs = [n_in // 256 * (144 if t == 12 else 210) for _, _, t in mats]
+        gbytes = sum(rb * n for rb, (_, n, _) in zip(rbs, mats))
+        copies = max(2, min(256, (512 << 20) // gbytes + 1))
+        Ws = [[qmag.DBuf(rb * n) for rb, (_, n, _) in zip(rbs, mats)] for _ in range(copies)]
+        for c, ws in enumerate(Ws):
+            for w, (_, n, t) in zip(ws, mats):
+                qmag.synth_weights(0xF300 + c, n_in * n, 0.02, t, w.ptr)
+        x = qmag.DBuf(4 * n_in)
+        qmag.synth_normal(0xF3, n_in, 0.0, 1.0, x.ptr)
+        ys = [qmag.DBuf(4 * n) for _, n, _ in mats]
+        k = len(mats)
+        no = (C.c_int * k)(*[n for _, n, _ in mats])
+        wt = (C.c_int * k)(*[t for _, _, t in mats])
+        yp = (C.c_void_p * k)(*[y.ptr for y in ys])
+        wps = [(C.c_void_p * k)(*[w.ptr for w in ws]) for ws in Ws]
+
+        def grouped():
+            for wp in wps:
+                L.qmag_matmul_group_dev(x.ptr, n_in, k, wp, no, wt, yp)
+
+        def separate():
+            for ws in Ws:
+                for w, y, (_, n, t) in zip(ws, ys, mats):
+                    L.qmag_matmul_dev(x.ptr, w.ptr, n_in, n, 1, t, y.ptr)
+
+        grouped()
+        separate()
+        ms_g, _ = gpu_loop(grouped, seconds)
+        ms_s, _ = gpu_loop(separate, seconds)
+        res[gname] = {"matrices": [m[0] for m in mats], "n_in": n_in, "weight_bytes": gbytes,
+                      "us_one_launch": ms_g * 1e3 / copies, "us_separate_calls": ms_s * 1e3 / copies,
+                      "weight_copies": copies}
+        for ws in Ws:
+            for w in ws:
+                w.close()
+    log("projection groups: " + ", ".join(f"{k} one launch {v['us_one_launch']:.2f} us vs separate "
+                                          f"{v['us_separate_calls']:.2f} us" for k, v in res.items()))
+    return res
 
 
 def aux_sampler(seconds: float, cpu_seconds: float) -> dict:

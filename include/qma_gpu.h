@@ -184,6 +184,21 @@ int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum,
 int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
                     float *out);
 
+/* Several matmuls over one activation vector in one launch (T = 1): out[i]
+   = W[i] . Q8_K(x) for i < n_mat <= QMAG_MV_GROUP_MAX, every matrix n_in
+   wide (a power of two from 256 to 8192) and of its own wtype (Q4_K, Q6_K or
+   QMAG_TYPE_Q6_K_R).  For the projections the engine computes from the same
+   x, one matmul() call each in the reference: q, k and v (nn.c:2111-2113),
+   and qkv, the attention gate and beta / alpha of the recurrent layers
+   (nn.c:2162, 2165-2170).  No counterpart in the reference: it saves the
+   per-launch cost of the separate calls.  W, n_out, wtype and out are host
+   arrays of n_mat entries (W and out holding device pointers).  Results are
+   bit-identical to separate qmag_matmul_dev calls.  QMAG_ERR_ARG when the
+   matrices need more than 65,536 waves together (call them separately). */
+#define QMAG_MV_GROUP_MAX 4
+int qmag_matmul_group_dev(const float *x, int n_in, int n_mat, const void *const *W, const int *n_out,
+                          const int *wtype, float *const *out);
+
 /* Repack n_out Q6_K rows of n_in weights (n_in a multiple of 2048) from the
    block layout (block_q6_K, qma.h; what the GGUF holds) into the row layout
    the matmul entries read fastest, for wtype QMAG_TYPE_Q6_K_R: per row, each

@@ -79,6 +79,18 @@ int launch_matvec(const int8_t *xq, const float *xd, const int16_t *xsum, const 
 // available for the row lengths matvec_x_supported() accepts
 bool matvec_x_supported(int n_in);
 int launch_repack_q6k(const void *src, void *dst, int n_in, int n_out, hipStream_t s);
+// up to QMAG_MV_GROUP_MAX matrices over one x at T = 1, one launch
+struct MvGroup {
+    const uint8_t *W[QMAG_MV_GROUP_MAX];
+    float *out[QMAG_MV_GROUP_MAX];
+    int n_out[QMAG_MV_GROUP_MAX];
+    int wtype[QMAG_MV_GROUP_MAX];
+    int wave0[QMAG_MV_GROUP_MAX + 1];   // first wave of each matrix; wave0[n] = all waves
+    int n;
+};
+constexpr int QMAG_MV_GROUP_MAX_WAVES = 1 << 16;
+int launch_matvec_group(const float *x, int n_in, int n_mat, const void *const *W, const int *n_out,
+                        const int *wtype, float *const *out, hipStream_t s);
 int launch_matvec_x(const float *x, const void *W, int n_in, int n_out, int wtype, float *out, hipStream_t s);
 // fp32 path of quants.c (qmag_quants.hip)
 int launch_dequant(const void *W, int wtype, long n, float *y, hipStream_t s);

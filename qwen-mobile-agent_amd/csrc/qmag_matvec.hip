@@ -77,9 +77,14 @@ struct RowTask<QMAG_TYPE_Q4_K> {
         q4_load_act(a, xq, xd, xs, ib, q);
     }
     // float contribution of this lane's task
+    // the task's value is rounded before any caller sums it (the empty asm
+    // keeps the compiler from fusing its last product into that sum, which
+    // it would do differently in different kernels)
     __device__ static float dot(const Raw &r, const Act &a, int q)
     {
-        return q4_task(r.hdr, r.q0, r.q1, a, q);
+        float p = q4_task(r.hdr, r.q0, r.q1, a, q);
+        __asm__ volatile("" : "+v"(p));
+        return p;
     }
 };
 
@@ -106,7 +111,9 @@ struct RowTask<QMAG_TYPE_Q6_K> {
     {
         const int part = q6_int_dot(r, a.a, q & 1);
         const int isum = group_sum_i<4>(part);
-        return q == 0 ? h2f(r.d) * a.xd * (float)isum : 0.0f;
+        float p = h2f(r.d) * a.xd * (float)isum;
+        __asm__ volatile("" : "+v"(p));             // rounded here, as for Q4_K
+        return q == 0 ? p : 0.0f;
     }
 };
 
@@ -245,7 +252,7 @@ __global__ __launch_bounds__(QMAG_MV_WG) void matvec_kernel(const uint8_t *__res
             for (int u = 0; u < U; u++) {
                 float v = 0.0f;
 #pragma unroll
-                for (int j = 0; j < TPL; j++) v += RT::dot(raw[u][j], act[j], q);
+                for (int j = 0; j < TPL; j++) v = __fadd_rn(v, RT::dot(raw[u][j], act[j], q));   // no contraction
                 v = group_sum<LPR>(v);
                 const int row = base + u * RPW + rw;
                 if (sub == 0 && row < n_out) out[(size_t)t * n_out + row] = v;
@@ -276,6 +283,143 @@ static int launch_mv_nb(const int8_t *xq, const float *xd, const int16_t *xsum, 
     else
         hipLaunchKernelGGL((matvec_kernel<WT, NB, false>), dim3(wgs), dim3(QMAG_MV_WG), 0, s,
                            (const uint8_t *)W, xq, xd, xsum, out, n_out, T, nullptr);
+    prof_end(PROF_MATVEC, s);
+    QMAG_HIP(hipGetLastError());
+    return QMAG_OK;
+}
+
+// Several matrices over the same x at T = 1 (the projections the engine
+// computes from one activation vector, nn.c:2111-2113, 2162-2170) in one
+// launch: waves are dealt to the matrices in order (matrix m takes waves
+// wave0[m] .. wave0[m+1]-1, one wave step of rows each, no grid stride), each
+// wave requests its rows with its matrix's row task, then every workgroup
+// computes Q8_K(x) into LDS exactly as the one-token kernel does, and each
+// wave finishes its rows with that kernel's dot and reduction: every output
+// is bit-identical to a separate qmag_matmul_dev call.
+template <int NB>
+__global__ __launch_bounds__(QMAG_MV_WG) void matvec_group_kernel(MvGroup g, const float *__restrict__ xf)
+{
+    using R4 = RowTask<QMAG_TYPE_Q4_K>;
+    using R6 = RowTask<QMAG_TYPE_Q6_K>;
+    using R6R = RowTask<QMAG_TYPE_Q6_K_R>;
+    constexpr int TPR = 4 * NB;
+    constexpr int LPR = TPR < 64 ? TPR : 64;
+    constexpr int TPL = TPR / LPR;
+    constexpr int RPW = 64 / LPR;
+    constexpr int U = QMAG_MV_U;
+    constexpr int N_IN = NB * QK_K;
+    __shared__ __align__(16) int8_t s_xq[N_IN];
+    __shared__ float s_xd[NB];
+    __shared__ __align__(16) int16_t s_xs[N_IN / 16];
+
+    const int lane = lane_id();
+    const int sub = lane % LPR, rw = lane / LPR;
+    const int q = sub & 3;
+    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    int m = 0;
+    while (m + 1 < g.n && wave >= g.wave0[m + 1]) m++;          // wave-uniform
+    const bool live = wave < g.wave0[g.n];
+    const int wt = g.wtype[m], n_out = g.n_out[m];
+    const uint8_t *W = g.W[m];
+    const int base = (wave - g.wave0[m]) * RPW * U;
+    constexpr size_t RB4 = (size_t)NB * Q4K_BYTES, RB6 = (size_t)NB * Q6K_BYTES;
+
+    typename R4::Raw r4[U][TPL];
+    typename R6::Raw r6[U][TPL];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int row = base + u * RPW + rw;
+#pragma unroll
+        for (int j = 0; j < TPL; j++) {
+            r4[u][j] = typename R4::Raw{};
+            r6[u][j] = typename R6::Raw{};
+            const int ib = (sub + LPR * j) >> 2;
+            if (live && row < n_out) {
+                if (wt == QMAG_TYPE_Q4_K) R4::load_raw(r4[u][j], W + (size_t)row * RB4, ib, q, NB);
+                else if (wt == QMAG_TYPE_Q6_K) R6::load_raw(r6[u][j], W + (size_t)row * RB6, ib, q, NB);
+                else R6R::load_raw(r6[u][j], W + (size_t)row * RB6, ib, q, NB);
+            }
+        }
+    }
+    const int wv = (int)(threadIdx.x >> 6);
+    for (int b = wv; b < NB; b += QMAG_MV_WG / 64) {
+        const Q8Lane r = q8k_quant_lane(ldg4(xf + b * QK_K + 4 * lane));
+        ((uint32_t *)(s_xq + b * QK_K))[lane] = r.packed;
+        if (lane == 0) s_xd[b] = r.d;
+        if ((lane & 3) == 0) s_xs[b * 16 + (lane >> 2)] = (int16_t)r.gsum;
+    }
+    __syncthreads();
+    if (!live) return;
+    float *out = g.out[m];
+    if (wt == QMAG_TYPE_Q4_K) {
+        typename R4::Act act[TPL];
+#pragma unroll
+        for (int j = 0; j < TPL; j++) R4::load_act(act[j], s_xq, s_xd, s_xs, (sub + LPR * j) >> 2, q);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float v = 0.0f;
+#pragma unroll
+            for (int j = 0; j < TPL; j++) v = __fadd_rn(v, R4::dot(r4[u][j], act[j], q));
+            v = group_sum<LPR>(v);
+            const int row = base + u * RPW + rw;
+            if (sub == 0 && row < n_out) out[row] = v;
+        }
+    } else {
+        typename R6::Act act[TPL];
+#pragma unroll
+        for (int j = 0; j < TPL; j++) R6::load_act(act[j], s_xq, s_xd, s_xs, (sub + LPR * j) >> 2, q);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float v = 0.0f;
+#pragma unroll
+            for (int j = 0; j < TPL; j++) v = __fadd_rn(v, R6::dot(r6[u][j], act[j], q));
+            v = group_sum<LPR>(v);
+            const int row = base + u * RPW + rw;
+            if (sub == 0 && row < n_out) out[row] = v;
+        }
+    }
+}
+
+int launch_matvec_group(const float *x, int n_in, int n_mat, const void *const *W, const int *n_out,
+                        const int *wtype, float *const *out, hipStream_t s)
+{
+    if (n_mat < 1 || n_mat > QMAG_MV_GROUP_MAX) return fail(QMAG_ERR_ARG, "matmul_group: n_mat=%d (1..%d)", n_mat, QMAG_MV_GROUP_MAX);
+    if (!x || !W || !n_out || !wtype || !out) return fail(QMAG_ERR_ARG, "matmul_group: null pointer");
+    const int nb = n_in / QK_K;
+    if (n_in <= 0 || n_in % QK_K || !(nb == 1 || nb == 2 || nb == 4 || nb == 8 || nb == 16 || nb == 32))
+        return fail(QMAG_ERR_ARG, "matmul_group: n_in=%d (a power of two from 256 to 8192)", n_in);
+    const int lpr = 4 * nb < 64 ? 4 * nb : 64, rows_per_wave = 64 / lpr * QMAG_MV_U;
+    MvGroup g{};
+    g.n = n_mat;
+    long waves = 0;
+    for (int i = 0; i < n_mat; i++) {
+        const int t = wtype[i];
+        if (t != QMAG_TYPE_Q4_K && t != QMAG_TYPE_Q6_K && t != QMAG_TYPE_Q6_K_R)
+            return fail(QMAG_ERR_ARG, "matmul_group: matrix %d: unsupported wtype %d", i, t);
+        if (!W[i] || !out[i] || n_out[i] <= 0) return fail(QMAG_ERR_ARG, "matmul_group: matrix %d: null or empty", i);
+        if (t == QMAG_TYPE_Q6_K_R && (n_in % (8 * QK_K) || ((uintptr_t)W[i] & 15)))
+            return fail(QMAG_ERR_ARG, "matmul_group: matrix %d: repacked Q6_K needs n_in %% 2048 == 0 and 16-byte aligned rows", i);
+        g.W[i] = (const uint8_t *)W[i];
+        g.out[i] = out[i];
+        g.n_out[i] = n_out[i];
+        g.wtype[i] = t;
+        g.wave0[i] = (int)waves;
+        waves += (n_out[i] + rows_per_wave - 1) / rows_per_wave;
+        if (waves > QMAG_MV_GROUP_MAX_WAVES)
+            return fail(QMAG_ERR_ARG, "matmul_group: %ld row steps exceed %d (call the matrices separately)", waves,
+                        QMAG_MV_GROUP_MAX_WAVES);
+    }
+    g.wave0[n_mat] = (int)waves;
+    const int wgs = (int)((waves + QMAG_MV_WG / 64 - 1) / (QMAG_MV_WG / 64));
+    prof_begin(PROF_MATVEC, s);
+    switch (nb) {
+    case 1: hipLaunchKernelGGL(matvec_group_kernel<1>, dim3(wgs), dim3(QMAG_MV_WG), 0, s, g, x); break;
+    case 2: hipLaunchKernelGGL(matvec_group_kernel<2>, dim3(wgs), dim3(QMAG_MV_WG), 0, s, g, x); break;
+    case 4: hipLaunchKernelGGL(matvec_group_kernel<4>, dim3(wgs), dim3(QMAG_MV_WG), 0, s, g, x); break;
+    case 8: hipLaunchKernelGGL(matvec_group_kernel<8>, dim3(wgs), dim3(QMAG_MV_WG), 0, s, g, x); break;
+    case 16: hipLaunchKernelGGL(matvec_group_kernel<16>, dim3(wgs), dim3(QMAG_MV_WG), 0, s, g, x); break;
+    default: hipLaunchKernelGGL(matvec_group_kernel<32>, dim3(wgs), dim3(QMAG_MV_WG), 0, s, g, x); break;
+    }
     prof_end(PROF_MATVEC, s);
     QMAG_HIP(hipGetLastError());
     return QMAG_OK;

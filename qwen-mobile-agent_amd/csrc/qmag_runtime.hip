@@ -359,6 +359,14 @@ int qmag_matmul_q8k_dev(const int8_t *xq, const float *xd, const int16_t *xsum, 
     return launch_matvec(xq, xd, xsum, W, n_in, n_out, T, wtype, out, g_ctx.stream);
 }
 
+int qmag_matmul_group_dev(const float *x, int n_in, int n_mat, const void *const *W, const int *n_out,
+                          const int *wtype, float *const *out)
+{
+    int st = require_ready();
+    if (st) return st;
+    return launch_matvec_group(x, n_in, n_mat, W, n_out, wtype, out, g_ctx.stream);
+}
+
 int qmag_repack_q6k_dev(const void *src, void *dst, int n_in, int n_out)
 {
     int st = require_ready();

@@ -54,6 +54,7 @@ SIGNATURES = {
     "qmag_matmul_q8k_dev": (C.c_int, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_matmul_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_repack_q6k_dev": (C.c_int, [P, P, C.c_int, C.c_int]),
+    "qmag_matmul_group_dev": (C.c_int, [P, C.c_int, C.c_int, P, P, P, P]),
     "qmag_matmul_noalloc_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_dequant_dev": (C.c_int, [P, C.c_int, C.c_int64, P]),
     "qmag_matmul_f32_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
@@ -268,6 +269,16 @@ def matmul_q8k_dev(xq, xd, xs, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> Non
 
 def matmul_dev(x: DBuf, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> None:
     check(lib().qmag_matmul_dev(x.ptr, W.ptr, n_in, n_out, T, wtype, out.ptr))
+
+
+def matmul_group_dev(x: DBuf, n_in: int, mats, outs) -> None:
+    """mats: [(W DBuf, n_out, wtype)], outs: [DBuf]; one launch for all."""
+    n = len(mats)
+    W = (P * n)(*[m[0].ptr for m in mats])
+    no = (C.c_int * n)(*[m[1] for m in mats])
+    wt = (C.c_int * n)(*[m[2] for m in mats])
+    out = (P * n)(*[o.ptr for o in outs])
+    check(lib().qmag_matmul_group_dev(x.ptr, n_in, n, W, no, wt, out))
 
 
 def repack_q6k_dev(src: DBuf, dst: DBuf, n_in: int, n_out: int) -> None:

@@ -14,7 +14,9 @@ oracle on the same bytes:
   wv and wqkv vary);
 * Q6_K rows repacked by qmag_repack_q6k_dev (a layout of this library):
   bit-identical matmul results to the block layout through every matmul
-  entry, the oracle's within 1e-4, and the documented byte order.
+  entry, the oracle's within 1e-4, and the documented byte order;
+* qmag_matmul_group_dev (the projections of one x in one launch): each
+  matrix's output bit-identical to a separate call, the oracle's within 1e-4.
 """
 import ctypes as C
 import threading
@@ -311,3 +313,66 @@ def test_q6k_repack_rejects_bad_arguments(qm):
     assert L.qmag_matmul_dev(x.ptr, W.ptr, 1024, 64, 1, qm.TYPE_Q6_K_R, out.ptr) == -2
     assert L.qmag_matmul_dev(x.ptr, R.ptr + 8, 2048, 64, 1, qm.TYPE_Q6_K_R, out.ptr) == -2
     assert L.qmag_repack_q6k_dev(W.ptr, R.ptr, 2048, 64) == 0
+
+
+GROUPS = [
+    # q, k, v of an attention layer (nn.c:2111-2113; wv's type varies)
+    (2048, [(8192, 12), (512, 12), (512, 14)]),
+    # qkv, gate, beta, alpha of a recurrent layer (nn.c:2162, 2165-2170)
+    (2048, [(8192, 14), (4096, 12), (32, 12), (32, 12)]),
+    # ragged row counts, a repacked Q6_K matrix, other row lengths
+    (2048, [(300, 14), (77, 270), (5, 12)]),
+    (4096, [(2048, 12), (33, 14)]),
+    (512, [(100, 12), (3, 14)]),
+    (8192, [(64, 14), (70, 12)]),
+]
+
+
+@pytest.mark.parametrize("n_in,mats", GROUPS)
+def test_matmul_group_matches_separate_calls(qm, orc, n_in, mats):
+    """qmag_matmul_group_dev (several matrices over one x, one launch) gives
+    each matrix the bits of a separate qmag_matmul_dev call, and the oracle's
+    result within 1e-4."""
+    x = orc.fill_normal(8000 + n_in, n_in, 0.0, 1.0)
+    xb = qm.DBuf.from_array(x)
+    bufs, hosts = [], []
+    for i, (n_out, t) in enumerate(mats):
+        W = orc.quantize(orc.fill_normal(8100 + 7 * i + n_in, n_in * n_out, 0.0, 0.02), 14 if t == 270 else t)
+        b = qm.DBuf.from_array(W)
+        if t == 270:
+            r = qm.DBuf(W.nbytes)
+            qm.repack_q6k_dev(b, r, n_in, n_out)
+            b = r
+        bufs.append(b)
+        hosts.append((W, 14 if t == 270 else t))
+    outs = [qm.DBuf(4 * n_out) for n_out, _ in mats]
+    qm.matmul_group_dev(xb, n_in, [(b, n, t) for b, (n, t) in zip(bufs, mats)], outs)
+    for b, o, (n_out, t), (W, th) in zip(bufs, outs, mats, hosts):
+        want = qm.DBuf(4 * n_out)
+        qm.matmul_dev(xb, b, n_in, n_out, 1, t, want)
+        got = o.download(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.download(np.uint32)), (n_out, t)
+        ref = orc.matmul_q8k(x, W, n_in, n_out, 1, th)[0]
+        assert max_rel_err(got, ref) < TOL
+
+
+def test_matmul_group_rejects_bad_arguments(qm):
+    """Group sizes outside 1..4, row lengths without a tiled form, unknown
+    types and empty matrices are argument errors."""
+    L = qm.lib()
+    x, W, y = qm.DBuf(4 * 2048), qm.DBuf(144 * 8 * 64), qm.DBuf(4 * 64)
+
+    def call(n_in, n, n_out=64, wtype=12):
+        Ws = (C.c_void_p * max(n, 1))(*([W.ptr] * max(n, 1)))
+        no = (C.c_int * max(n, 1))(*([n_out] * max(n, 1)))
+        wt = (C.c_int * max(n, 1))(*([wtype] * max(n, 1)))
+        ys = (C.c_void_p * max(n, 1))(*([y.ptr] * max(n, 1)))
+        return L.qmag_matmul_group_dev(x.ptr, n_in, n, Ws, no, wt, ys)
+
+    assert call(2048, 0) == -2
+    assert call(2048, 5) == -2
+    assert call(768, 1) == -2
+    assert call(2048, 1, wtype=13) == -2
+    assert call(2048, 1, n_out=0) == -2
+    assert call(1024, 1, wtype=270) == -2
+    assert call(2048, 2) == 0
