@@ -8,6 +8,11 @@
 // a wave covers 64/LPR rows per step; each lane keeps its task's activation
 // slice in registers across rows and issues its weight loads for U row
 // steps before consuming any of them.  Row sums use DPP/permlane reductions.
+//
+// Also here: Q6_K rows repacked into aligned planes (QMAG_TYPE_Q6_K_R, same
+// bytes and results, for large matrices such as the LM head), and one launch
+// for several matrices over the same x (the projections of one activation
+// vector), bit-identical to separate calls.
 #include "qmag_internal.h"
 
 // Launch shape of the tiled matvec: wave steps of rows in flight per wave,
