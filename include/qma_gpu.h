@@ -194,7 +194,9 @@ int qmag_matmul_dev(const float *x, const void *W, int n_in, int n_out, int T, i
    per-launch cost of the separate calls.  W, n_out, wtype and out are host
    arrays of n_mat entries (W and out holding device pointers).  Results are
    bit-identical to separate qmag_matmul_dev calls.  QMAG_ERR_ARG when the
-   matrices need more than 65,536 waves together (call them separately). */
+   matrices need more than 65,536 waves together (call them separately).
+   It allocates nothing: x is quantised inside the kernel and the matrix
+   table travels as kernel arguments. */
 #define QMAG_MV_GROUP_MAX 4
 int qmag_matmul_group_dev(const float *x, int n_in, int n_mat, const void *const *W, const int *n_out,
                           const int *wtype, float *const *out);
