@@ -364,6 +364,7 @@ int qmag_matmul_group_dev(const float *x, int n_in, int n_mat, const void *const
 {
     int st = require_ready();
     if (st) return st;
+    ProfSuspend quiet;        // per-kernel event timing allocates events: off here
     return launch_matvec_group(x, n_in, n_mat, W, n_out, wtype, out, g_ctx.stream);
 }
 
