@@ -180,6 +180,26 @@ int launch_repack_q6k(const void *src, void *dst, int n_in, int n_out, hipStream
     return QMAG_OK;
 }
 
+// Q8_K of one activation vector of NB blocks into a workgroup's LDS: each
+// half-wave quantises one 256-block (8 values per lane, q8k_quant_half, the
+// same bits as q8k_quant_kernel), so a wave covers two blocks at once.
+template <int NB>
+__device__ __forceinline__ void q8k_x_to_lds(const float *__restrict__ xf, int8_t *s_xq, float *s_xd,
+                                             int16_t *s_xs)
+{
+    const int lane = lane_id(), wv = (int)(threadIdx.x >> 6), hl = lane >> 5, L = lane & 31;
+    for (int b0 = 2 * wv; b0 < NB; b0 += 2 * (QMAG_MV_WG / 64)) {
+        const int b = b0 + hl;
+        const int bb = b < NB ? b : NB - 1;    // the half past the last block (NB = 1) stores nothing
+        const Q8Lane2 r = q8k_quant_half(ldg4(xf + bb * QK_K + 8 * L), ldg4(xf + bb * QK_K + 8 * L + 4));
+        if (b < NB) {
+            ((uint2 *)(s_xq + b * QK_K))[L] = make_uint2(r.packed[0], r.packed[1]);
+            if (L == 0) s_xd[b] = r.d;
+            if ((L & 1) == 0) s_xs[b * 16 + (L >> 1)] = (int16_t)r.gsum;
+        }
+    }
+}
+
 // ONE_TOKEN: T = 1, the activation operand is loaded once per lane.  XF
 // (with ONE_TOKEN): the kernel takes x itself and every workgroup computes
 // its Q8_K into LDS with the same per-block routine as q8k_quant_kernel
@@ -229,13 +249,7 @@ __global__ __launch_bounds__(QMAG_MV_WG) void matvec_kernel(const uint8_t *__res
         __shared__ float s_xd[NB];
         __shared__ __align__(16) int16_t s_xs[N_IN / 16];
         load_rows(base0);                       // the weights are in flight during the quantisation
-        const int wv = (int)(threadIdx.x >> 6);
-        for (int b = wv; b < NB; b += QMAG_MV_WG / 64) {
-            const Q8Lane r = q8k_quant_lane(ldg4(xf + b * QK_K + 4 * lane));
-            ((uint32_t *)(s_xq + b * QK_K))[lane] = r.packed;
-            if (lane == 0) s_xd[b] = r.d;
-            if ((lane & 3) == 0) s_xs[b * 16 + (lane >> 2)] = (int16_t)r.gsum;
-        }
+        q8k_x_to_lds<NB>(xf, s_xq, s_xd, s_xs);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < TPL; j++) RT::load_act(act[j], s_xq, s_xd, s_xs, (sub + LPR * j) >> 2, q);
@@ -346,13 +360,7 @@ __global__ __launch_bounds__(QMAG_MV_WG) void matvec_group_kernel(MvGroup g, con
             }
         }
     }
-    const int wv = (int)(threadIdx.x >> 6);
-    for (int b = wv; b < NB; b += QMAG_MV_WG / 64) {
-        const Q8Lane r = q8k_quant_lane(ldg4(xf + b * QK_K + 4 * lane));
-        ((uint32_t *)(s_xq + b * QK_K))[lane] = r.packed;
-        if (lane == 0) s_xd[b] = r.d;
-        if ((lane & 3) == 0) s_xs[b * 16 + (lane >> 2)] = (int16_t)r.gsum;
-    }
+    q8k_x_to_lds<NB>(xf, s_xq, s_xd, s_xs);
     __syncthreads();
     if (!live) return;
     float *out = g.out[m];
