@@ -44,6 +44,9 @@ extern "C" {
 #define QMAG_ERR_ARG (-2)      /* unsupported shape / type / null pointer    */
 #define QMAG_ERR_NODEV (-3)    /* no gfx950 device, or qmag_init not called  */
 #define QMAG_ERR_KERNEL (-4)   /* a kernel reported an internal guard trip   */
+#define QMAG_ERR_REPLAYED (-5) /* decode calls were re-run after an expired
+                                  wait; work queued after them (logits) is
+                                  stale and must be queued again            */
 /* Buffers passed to the device entries must stay valid until the next
    qmag_sync or qmag_d2h: the library may re-run the calls issued since the
    previous one (see qmag_fused_recoveries).  Only those MoE calls are re-run:
@@ -420,7 +423,13 @@ int qmag_sampler_candidates_dev(int n_vocab, const float *logits, const qmag_sam
    top-p cut, one xorshift64* draw (s->seed advances) and the pick joining
    s->last_tokens (the last 64 kept).  Replaces the pair at agent.c:935-955
    when no grammar mask runs (tool_mode off); with the mask, call
-   qmag_sampler_candidates_dev and the host's sampler_pick on its 40. */
+   qmag_sampler_candidates_dev and the host's sampler_pick on its 40.
+   Both sampler entries first settle persistent decode calls still pending
+   (as qmag_sync does); if that re-ran any of them after an expired wait,
+   the logits, computed on the stream from their earlier outputs, are stale:
+   the call then samples nothing, leaves *s unchanged and returns
+   QMAG_ERR_REPLAYED, and the caller recomputes the logits (the LM head) and
+   calls again. */
 int qmag_sampler_sample_dev(int n_vocab, const float *logits, qmag_sampler *s, int max_k, float top_p,
                             int *token);
 

@@ -418,8 +418,10 @@ __device__ __forceinline__ int q6_int_dot(const Q6Raw &r, const Q6Act &a, int l1
 
 // ---------------------------------------------------------- routing ----
 // The reference's softmax (nn.c:517-527) turns every probability into NaN
-// when one logit is NaN or +Inf (its term is NaN), or when every logit is at
-// or below its -1e30 starting maximum (the sum is 0).  Then no `p > -1e30`
+// when one logit is NaN or +Inf (its term is NaN), or when every logit is
+// strictly below its -1e30 starting maximum (every term underflows to 0, and
+// so does the sum; a logit of exactly -1e30 leaves the maximum there and
+// makes a term expf(0) = 1, so routing stays ordinary).  Then no `p > -1e30`
 // test of the top-K scan holds and every pick is expert 0 with value -1e30
 // (nn.c:529-533), renormalised to -1e30 / (K * -1e30) summed in pick order.
 // The E <= 256 logits sit 4 per lane of one wave, expert lane + 64j.
@@ -434,7 +436,7 @@ __device__ __forceinline__ bool route_degenerate(const float (&l)[4], int E)
             mx = fmaxf(mx, l[j]);
         }
     }
-    return __ballot(bad) != 0 || group_max<64>(mx) <= -1e30f;
+    return __ballot(bad) != 0 || group_max<64>(mx) < -1e30f;
 }
 __device__ __forceinline__ float route_degenerate_weight(int K)
 {

@@ -308,10 +308,17 @@ const uint8_t *get_locked(qmag_ecache *c, std::unique_lock<std::mutex> &lk, int 
     const int32_t key = key_of(layer, expert);
     c->clock++;
     if (c->last_used >= 0 && c->slot[c->last_used].state == EC_READY) c->last_used = -1;
-    if (c->n_slots > 0) {
+    while (c->n_slots > 0) {
         const int si = lookup(c, key);
-        if (si >= 0) {
-            c->done.wait(lk, [&] { return c->slot[si].state != EC_INFLIGHT; });
+        if (si < 0) break;
+        {
+            // Wait for the read in flight.  While this call waits the slot can
+            // change hands (the read fails and another call drops it, or it
+            // lands and is evicted and claimed for another record): then the
+            // key is looked up again instead of the slot's new record being
+            // returned under this key.
+            c->done.wait(lk, [&] { return c->slot[si].key != key || c->slot[si].state != EC_INFLIGHT; });
+            if (c->slot[si].key != key) continue;
             if (c->slot[si].state != EC_READY) {
                 drop(c, si);
                 issue_next(c);

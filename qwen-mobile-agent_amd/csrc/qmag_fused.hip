@@ -428,9 +428,9 @@ __device__ void route_topk(const float (&lg)[4], int E, int K, int &my_sel, floa
     if (!topk_picks<false>(v, id, K, lane, sel, my_key)) topk_picks<true>(v, id, K, lane, sel, my_key);
     const float l0 = key2f(__builtin_amdgcn_readfirstlane(my_key));
     // the reference's softmax is NaN throughout when a logit is NaN or +Inf,
-    // or when every logit is at or below -1e30 (see route_degenerate): then
-    // it picks expert 0 K times
-    if (any_nan || !(l0 < INFINITY) || l0 <= -1e30f) {
+    // or when every logit is strictly below -1e30 (see route_degenerate):
+    // then it picks expert 0 K times
+    if (any_nan || !(l0 < INFINITY) || l0 < -1e30f) {
         if (lane < K) my_sel = 0;
         my_w = route_degenerate_weight(K);
         return;
@@ -949,7 +949,8 @@ bool fused_pending() { return g_pending; }
 // are then re-run from launch e on through the launch sequence, in-place
 // calls first restored from the copy of their input taken before they ran.
 struct FusedCall {
-    std::vector<qmag_moe_layer> layers;
+    size_t layer0 = 0;                    // the call's descriptors: g_log_layers[layer0 .. + n_layer)
+    int n_layer = 0;
     float *x = nullptr, *out = nullptr;   // out == nullptr: the stack (x updated in place)
     int n_tok = 0;
     int lpt = 1;                          // persistent launches per token (fused runs of a mixed stack)
@@ -957,16 +958,35 @@ struct FusedCall {
     int snap = -1;                        // snapshot slot holding the input rows, or -1
 };
 // At most LOG_CALLS calls, SNAP_SLOTS of them in place, between status
-// checks; a call that would exceed either first checks (a stream sync).
-constexpr int LOG_CALLS = 1024, SNAP_SLOTS = 8;
+// checks; a call that would exceed either first checks (a stream sync, so
+// it is kept rare: a one-layer call adds one entry and one descriptor to
+// storage whose capacity persists, no allocation per call).
+constexpr int LOG_CALLS = 16384, SNAP_SLOTS = 8;
 static std::vector<FusedCall> g_log;
+static std::vector<qmag_moe_layer> g_log_layers;
 static int g_snap_used = 0;
 static float *g_snap[SNAP_SLOTS] = {};
 static size_t g_snap_bytes[SNAP_SLOTS] = {};
 static long g_recovered = 0;
 static int g_test_abort = 0;
 
-static int replay(const std::vector<FusedCall> &log, unsigned e, hipStream_t s)
+// append a call to the log; its descriptors are shared with the previous
+// entry when they are the same (a stack decoded step after step)
+static void log_call(FusedCall &c, const qmag_moe_layer *L, int n_layer)
+{
+    c.n_layer = n_layer;
+    if (!g_log.empty() && g_log.back().n_layer == n_layer &&
+        memcmp(g_log_layers.data() + g_log.back().layer0, L, sizeof(qmag_moe_layer) * (size_t)n_layer) == 0) {
+        c.layer0 = g_log.back().layer0;
+    } else {
+        c.layer0 = g_log_layers.size();
+        g_log_layers.insert(g_log_layers.end(), L, L + n_layer);
+    }
+    g_log.push_back(c);
+}
+
+static int replay(const std::vector<FusedCall> &log, const std::vector<qmag_moe_layer> &layers, unsigned e,
+                  hipStream_t s)
 {
     const size_t N = fused::N;
     for (const FusedCall &c : log) {
@@ -976,15 +996,16 @@ static int replay(const std::vector<FusedCall> &log, unsigned e, hipStream_t s)
         if (c.snap >= 0)
             QMAG_HIP(hipMemcpyAsync(c.x + t0 * N, g_snap[c.snap] + t0 * N, sizeof(float) * rows,
                                     hipMemcpyDeviceToDevice, s));
+        const qmag_moe_layer *cl = layers.data() + c.layer0;
         for (int t = t0; t < c.n_tok; t++) {
             float *xt = c.x + t * N;
             if (!c.out) {
-                for (const qmag_moe_layer &L : c.layers) {
-                    int st = moe_ffn(&L, xt, xt, 1, xt, s);
+                for (int l = 0; l < c.n_layer; l++) {
+                    int st = moe_ffn(&cl[l], xt, xt, 1, xt, s);
                     if (st) return st;
                 }
             } else {
-                int st = moe_ffn(&c.layers[0], xt, c.out + t * N, 1, nullptr, s);
+                int st = moe_ffn(&cl[0], xt, c.out + t * N, 1, nullptr, s);
                 if (st) return st;
             }
         }
@@ -999,19 +1020,26 @@ int fused_status()
     g_pending = false;
     if (!g_abort) {
         g_log.clear();
+        g_log_layers.clear();
         g_snap_used = 0;
         return QMAG_OK;
     }
     QMAG_HIP(hipStreamSynchronize(ctx().stream));
     int word = 0;
     QMAG_HIP(hipMemcpy(&word, g_abort, sizeof(int), hipMemcpyDeviceToHost));
-    std::vector<FusedCall> log;
-    log.swap(g_log);
     g_snap_used = 0;
-    if (word == 0) return QMAG_OK;
+    if (word == 0) {                 // the common case: keep the storage's capacity
+        g_log.clear();
+        g_log_layers.clear();
+        return QMAG_OK;
+    }
+    std::vector<FusedCall> log;
+    std::vector<qmag_moe_layer> layers;
+    log.swap(g_log);
+    layers.swap(g_log_layers);
     int st = rearm();
     if (st) return st;
-    st = replay(log, (unsigned)word - 1u, ctx().stream);
+    st = replay(log, layers, (unsigned)word - 1u, ctx().stream);
     if (st) return st;
     g_recovered++;
     return QMAG_OK;
@@ -1128,6 +1156,24 @@ static int fused_launch(const qmag_moe_layer *L, const qmag_moe_layer *dl, int n
     return QMAG_OK;
 }
 
+// copy n_tok input rows at x into the next snapshot slot (grown as needed)
+static int take_snapshot(const float *x, int n_tok, hipStream_t s, int *slot_out)
+{
+    const int slot = g_snap_used++;
+    const size_t need = sizeof(float) * fused::N * (size_t)n_tok;
+    if (need > g_snap_bytes[slot]) {
+        QMAG_HIP(hipStreamSynchronize(s));
+        if (g_snap[slot]) QMAG_HIP(hipFree(g_snap[slot]));
+        g_snap[slot] = nullptr;
+        g_snap_bytes[slot] = 0;
+        QMAG_HIP(hipMalloc(&g_snap[slot], need));
+        g_snap_bytes[slot] = need;
+    }
+    QMAG_HIP(hipMemcpyAsync(g_snap[slot], x, need, hipMemcpyDeviceToDevice, s));
+    *slot_out = slot;
+    return QMAG_OK;
+}
+
 int fused_call(const qmag_moe_layer *L, int n_layer, float *x, float *out, int n_tok, hipStream_t s)
 {
     if (out && n_layer != 1) return fail(QMAG_ERR_ARG, "fused: out mode needs exactly one layer");
@@ -1146,26 +1192,15 @@ int fused_call(const qmag_moe_layer *L, int n_layer, float *x, float *out, int n
     int st = fused_prepare(L, n_layer, s, &dl);
     if (st) return st;
     FusedCall c;
-    c.layers.assign(L, L + n_layer);
     c.x = x;
     c.out = out;
     c.n_tok = n_tok;
     c.first_epoch = g_epoch;
     if (in_place) {                     // keep the input to replay from
-        const int slot = g_snap_used++;
-        const size_t need = sizeof(float) * fused::N * (size_t)n_tok;
-        if (need > g_snap_bytes[slot]) {
-            QMAG_HIP(hipStreamSynchronize(s));
-            if (g_snap[slot]) QMAG_HIP(hipFree(g_snap[slot]));
-            g_snap[slot] = nullptr;
-            g_snap_bytes[slot] = 0;
-            QMAG_HIP(hipMalloc(&g_snap[slot], need));
-            g_snap_bytes[slot] = need;
-        }
-        QMAG_HIP(hipMemcpyAsync(g_snap[slot], x, need, hipMemcpyDeviceToDevice, s));
-        c.snap = slot;
+        st = take_snapshot(x, n_tok, s, &c.snap);
+        if (st) return st;
     }
-    g_log.push_back(std::move(c));
+    log_call(c, L, n_layer);
     for (int t = 0; t < n_tok; t++) {
         st = fused_launch(L, dl, n_layer, x + (size_t)t * fused::N, out ? out + (size_t)t * fused::N : nullptr, s);
         if (st) return st;
@@ -1178,9 +1213,12 @@ int fused_call(const qmag_moe_layer *L, int n_layer, float *x, float *out, int n
 // the maximal runs of consecutive layers it can take go through it, the other
 // layers through the launch sequence, token by token in layer order.  The
 // whole stack's descriptors are uploaded once and each run reads its slice.
-// One log entry and one input snapshot per token cover the token's launches,
-// so an expired wait replays the token's whole stack through the launch
-// sequence.  Returns 1 (nothing launched) when no layer qualifies.
+// One log entry and one input snapshot cover a whole call (up to 2^22
+// persistent launches; a longer call is cut into such chunks of tokens):
+// token t's nf persistent launches are consecutive epochs, so an expired wait
+// of epoch e replays tokens (e - first) / nf on through the launch sequence,
+// each through the whole stack.  Returns 1 (nothing launched) when no layer
+// qualifies.
 int fused_stack_runs(const qmag_moe_layer *L, int n_layer, float *x, int n_tok, hipStream_t s)
 {
     if (n_layer < 2 || n_layer > 256) return 1;
@@ -1201,12 +1239,15 @@ int fused_stack_runs(const qmag_moe_layer *L, int n_layer, float *x, int n_tok, 
     int nf = 0;
     for (char f : rf) nf += f;
     if (nf == 0) return 1;
+    if (n_tok <= 0 || n_tok >= (1 << 23)) return fail(QMAG_ERR_ARG, "fused: n_tok=%d", n_tok);
     const qmag_moe_layer *dl = nullptr;
     int st = fused_prepare(L, n_layer, s, &dl);
     if (st) return st;
-    for (int t = 0; t < n_tok; t++) {
-        float *xt = x + (size_t)t * fused::N;
-        const bool wraps = g_epoch + (unsigned)nf >= (1u << 24);
+    const int chunk = (1 << 22) / nf;
+    for (int t0 = 0; t0 < n_tok; t0 += chunk) {
+        const int nt = n_tok - t0 < chunk ? n_tok - t0 : chunk;
+        float *xc = x + (size_t)t0 * fused::N;
+        const bool wraps = g_epoch + (unsigned)(nt * nf) >= (1u << 24);
         if (g_log.size() >= (size_t)LOG_CALLS || g_snap_used == SNAP_SLOTS || wraps) {
             st = fused_status();
             if (st) return st;
@@ -1216,32 +1257,24 @@ int fused_stack_runs(const qmag_moe_layer *L, int n_layer, float *x, int n_tok, 
             }
         }
         FusedCall c;
-        c.layers.assign(L, L + n_layer);
-        c.x = xt;
-        c.n_tok = 1;
+        c.x = xc;
+        c.n_tok = nt;
         c.lpt = nf;
         c.first_epoch = g_epoch;
-        const int slot = g_snap_used++;
-        const size_t need = sizeof(float) * fused::N;
-        if (need > g_snap_bytes[slot]) {
-            QMAG_HIP(hipStreamSynchronize(s));
-            if (g_snap[slot]) QMAG_HIP(hipFree(g_snap[slot]));
-            g_snap[slot] = nullptr;
-            g_snap_bytes[slot] = 0;
-            QMAG_HIP(hipMalloc(&g_snap[slot], need));
-            g_snap_bytes[slot] = need;
-        }
-        QMAG_HIP(hipMemcpyAsync(g_snap[slot], xt, need, hipMemcpyDeviceToDevice, s));
-        c.snap = slot;
-        g_log.push_back(std::move(c));
-        for (size_t r = 0; r < rb.size(); r++) {
-            if (rf[r]) {
-                st = fused_launch(L + rb[r], dl + rb[r], re[r] - rb[r], xt, nullptr, s);
-                if (st) return st;
-            } else {
-                for (int l = rb[r]; l < re[r]; l++) {
-                    st = moe_ffn(&L[l], xt, xt, 1, xt, s);
+        st = take_snapshot(xc, nt, s, &c.snap);
+        if (st) return st;
+        log_call(c, L, n_layer);
+        for (int t = 0; t < nt; t++) {
+            float *xt = xc + (size_t)t * fused::N;
+            for (size_t r = 0; r < rb.size(); r++) {
+                if (rf[r]) {
+                    st = fused_launch(L + rb[r], dl + rb[r], re[r] - rb[r], xt, nullptr, s);
                     if (st) return st;
+                } else {
+                    for (int l = rb[r]; l < re[r]; l++) {
+                        st = moe_ffn(&L[l], xt, xt, 1, xt, s);
+                        if (st) return st;
+                    }
                 }
             }
         }

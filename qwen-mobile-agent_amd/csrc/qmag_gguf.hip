@@ -393,17 +393,42 @@ int qmag_gguf_fetch_expert(void *user, int layer, int expert, uint8_t *dst)
 
 int qmag_gguf_expert_record_bytes(const qmag_gguf *g, size_t *rec)
 {
-    // the largest layer's record (nn.c:1601-1605): down types vary per layer
+    // The largest layer's record (nn.c:1601-1605): down types vary per
+    // layer.  Every blk.N.ffn_{gate,up,down}_exps tensor of the table counts,
+    // wherever its layer lies (a gap in the layer numbers does not end the
+    // scan), and a layer with only part of the triple fails the query: the
+    // fetch callback copies whatever the table holds, so the bound must cover
+    // every layer it can be asked for.
     if (!g || !rec) return err(QMAG_ERR_ARG, "gguf: bad argument");
+    static const char *const kinds[] = {".ffn_gate_exps.weight", ".ffn_up_exps.weight", ".ffn_down_exps.weight"};
+    std::unordered_map<long, int> seen;          // layer -> bit mask of the kinds present
+    for (const GgufTensor &t : g->tensors) {
+        if (t.name.compare(0, 4, "blk.") != 0) continue;
+        const size_t dot = t.name.find('.', 4);
+        if (dot == std::string::npos || dot == 4 || dot > 13) continue;
+        long il = 0;
+        bool digits = true;
+        for (size_t i = 4; i < dot; i++) {
+            if (t.name[i] < '0' || t.name[i] > '9') digits = false;
+            else il = il * 10 + (t.name[i] - '0');
+        }
+        if (!digits) continue;
+        for (int k = 0; k < 3; k++)
+            if (t.name.compare(dot, std::string::npos, kinds[k]) == 0) seen[il] |= 1 << k;
+    }
     size_t best = 0;
-    for (int il = 0;; il++) {
+    for (const auto &kv : seen) {
+        if (kv.second != 7 || kv.first > INT32_MAX)
+            return err(QMAG_ERR_ARG, "gguf: layer %ld has an incomplete expert tensor triple (gate/up/down mask %d)",
+                       kv.first, kv.second);
         const GgufTensor *t[3];
-        if (expert_slabs(g, il, 0, t)) break;
+        if (expert_slabs(g, (int)kv.first, 0, t))
+            return err(QMAG_ERR_ARG, "gguf: layer %ld expert tensors disagree on the expert count", kv.first);
         size_t r = 0;
         for (int i = 0; i < 3; i++) r += t[i]->nbytes / (size_t)t[i]->ne[2];
         if (r > best) best = r;
     }
-    if (!best) return err(QMAG_ERR_ARG, "gguf: no blk.0 expert tensors");
+    if (!best) return err(QMAG_ERR_ARG, "gguf: no expert tensors");
     *rec = best;
     return QMAG_OK;
 }

@@ -594,11 +594,21 @@ static int sample_run(int n_vocab, const float *logits, const qmag_sampler *s, i
     const int n_chunks = (n_vocab + SAMP_CHUNK - 1) / SAMP_CHUNK;
     hipStream_t st = ctx().stream;
     std::lock_guard<std::mutex> guard(g_samp_mu);
-    // logits computed from persistent-decode outputs: have any expired wait
-    // of those launches recovered first (qmag_d2h does the same)
+    // Logits computed from persistent-decode outputs: have any expired wait
+    // of those launches recovered first (qmag_d2h does the same).  A recovery
+    // re-runs the decode calls but not the work queued after them, such as
+    // the LM head that produced these logits from their earlier (partly
+    // unwritten) outputs: then nothing is sampled and the caller is told to
+    // recompute the logits.
     if (fused_pending()) {
+        const long r0 = fused_recoveries();
         const int fst = fused_status();
         if (fst) return fst;
+        if (fused_recoveries() != r0)
+            return fail(QMAG_ERR_REPLAYED,
+                        "sampler: persistent decode calls queued before these logits were re-run after an "
+                        "expired wait; logits computed from their earlier outputs are stale: recompute them "
+                        "and sample again");
     }
     const size_t cand_bytes = sizeof(uint64_t) * (size_t)SAMP_MAX_CHUNKS * SAMP_MAX_K;
     int wst = QMAG_OK;

@@ -121,3 +121,31 @@ def test_moe_layer_needs_its_tensors(qmlib, small_model, tmp_path):
     with pytest.raises(qmlib.QmagError, match="unexpected types or shapes"):
         g.upload_moe_layer(0)
     g.close()
+
+
+def test_record_bytes_cover_every_layer(qmlib, orc, tmp_path):
+    """The expert record bound covers every layer of the tensor table, not
+    only the first contiguous run: with blk.1 missing, blk.2's larger record
+    (Q6_K down against blk.0's Q4_K) is the bound.  A layer holding only part
+    of its gate/up/down triple fails the query instead of being skipped."""
+    N, F, E, K = 256, 256, 8, 2
+    l0 = make_host_layer(orc, seed=140, n_embd=N, n_ff=F, n_expert=E, n_used=K, t_down=12)
+    l2 = make_host_layer(orc, seed=142, n_embd=N, n_ff=F, n_expert=E, n_used=K, t_down=14)
+    t0 = gw.moe_model_tensors([l0])
+    t2 = [(n.replace("blk.0.", "blk.2."), ty, d, b) for n, ty, d, b in gw.moe_model_tensors([l0, l2])[8:]]
+    t2 = [(n.replace("blk.1.", "blk.2."), ty, d, b) for n, ty, d, b in t2]
+    p = tmp_path / "gap.gguf"
+    gw.write_gguf(p, gw.qwen35moe_metadata(3, N, E, K, F), t0 + t2)
+    g = qmlib.Gguf(str(p))
+    q4 = 2 * F * (N // 256) * 144 + N * (F // 256) * 144
+    q6 = 2 * F * (N // 256) * 144 + N * (F // 256) * 210
+    assert g.expert_record_bytes() == q6 > q4
+    g.close()
+    # blk.2 without its down tensor: the triple is incomplete
+    p2 = tmp_path / "partial.gguf"
+    gw.write_gguf(p2, gw.qwen35moe_metadata(3, N, E, K, F),
+                  t0 + [t for t in t2 if "ffn_down_exps" not in t[0]])
+    g = qmlib.Gguf(str(p2))
+    with pytest.raises(qmlib.QmagError, match="layer 2 has an incomplete expert tensor triple"):
+        g.expert_record_bytes()
+    g.close()

@@ -194,6 +194,53 @@ def test_paged_layer_equals_resident(qm, orc, tmp_path):
         g.close()
 
 
+def test_paged_layer_vs_oracle(qm, orc, tmp_path):
+    """The paged layer (experts through the cache, nn.c:553-571 and 677-694)
+    against the oracle's moe_ffn on the bytes the GGUF file holds, stage by
+    stage: logits, selection and weights, the shared gate, h of every slot
+    and the output (from the device's own h, as the staged check of the
+    resident path does), for T = 1 and 3, with evictions between calls and
+    with reader threads on.  Two qwen35moe-shaped layers, Q6_K then Q4_K
+    down."""
+    from test_gpu_moe import check_layer_staged
+    N, F, E, K = 2048, 512, 16, 8
+    path = tmp_path / "m.gguf"
+    host = _write(orc, path, 2, N, F, E, K)
+    g = qm.Gguf(str(path))
+    dev = [g.upload_moe_layer(il) for il in range(2)]
+    paged = []
+    for L in dev:
+        P_ = qm.MoeLayer()
+        C.memmove(C.byref(P_), C.byref(L), C.sizeof(L))
+        P_.gate_exps = P_.up_exps = P_.down_exps = None
+        paged.append(P_)
+    rec = g.expert_record_bytes()
+    c = qm.ECache(10 * rec, rec, fetch=qm.gguf_fetch_fn(), user=g.h)
+
+    def run_paged(il):
+        def run(x, T):
+            xb = qm.DBuf.from_array(x)
+            ob = qm.DBuf(4 * T * N)
+            c.moe_ffn_paged(paged[il], il, xb.ptr, ob.ptr, T)
+            return ob.download(np.float32).reshape(T, N)
+        return run
+
+    try:
+        for threads in (0, 3):
+            if threads:
+                c.io_start(threads, 2)
+            for il, hl in enumerate(host):
+                for T in (1, 3):
+                    x = orc.fill_normal(700 + 10 * il + T + threads, T * N, 0.0, 1.0)
+                    check_layer_staged(qm, orc, None, hl, x, T, run=run_paged(il))
+        assert c.stats()["evictions"] > 0
+    finally:
+        c.close()
+        for L in dev:
+            qm.Gguf.free_moe_layer(L)
+        g.close()
+
+
 def test_paged_layer_rejects_small_records(qm, orc, small):
     g = qm.Gguf(str(small))
     L = g.upload_moe_layer(0)
@@ -254,6 +301,69 @@ def test_concurrent_gets_of_hinted_records(qm, orc, small):
         g.close()
 
 
+def test_waiter_does_not_take_a_reclaimed_slot(qm, orc, small):
+    """A get that waits for a record in flight must not return whatever the
+    slot holds when it wakes.  The reader thread's fetch of one record fails
+    after a delay while a second thread keeps asking for another record; the
+    only slot it can claim is the failed one.  Whichever thread takes the lock
+    first, the waiter for the failing record gets nothing (never the other
+    record's slot), and the other record's bytes are its own."""
+    import threading
+    import time
+    g = qm.Gguf(str(small))
+    rec = g.expert_record_bytes()
+    recs = _records(g, 2)
+    FAIL = 7
+
+    def fetch(user, layer, expert, dst):
+        if expert == FAIL:
+            time.sleep(0.03)
+            return -1
+        b = recs.get((layer, expert))
+        if b is None:
+            return -1
+        C.memmove(dst, b.ctypes.data, b.size)
+        return 0
+
+    c = qm.ECache(4 * rec, rec, fetch=fetch)               # 4 slots
+    c.io_start(1, 1)
+    wrong = []
+    try:
+        for rnd in range(12):
+            c.release()
+            for e in (0, 1, 2):                             # three slots held: one victim left
+                assert c.hold(0, e)
+            c.prefetch(0, [FAIL])                           # the reader thread's read fails
+            res = {}
+
+            def waiter():
+                res["a"] = c.hold(0, FAIL)
+
+            def filler():
+                t_end = time.time() + 2.0
+                while time.time() < t_end:
+                    p = c.hold(0, 20 + rnd)
+                    if p:
+                        res["c"] = p
+                        return
+
+            ta, tc = threading.Thread(target=waiter), threading.Thread(target=filler)
+            ta.start()
+            time.sleep(0.005)
+            tc.start()
+            ta.join()
+            tc.join()
+            if res.get("a"):
+                wrong.append((rnd, res["a"]))
+            assert res.get("c"), rnd
+            _check_bytes(qm, recs, (0, 20 + rnd), res["c"], rec)
+            c.drain()
+    finally:
+        c.close()
+        g.close()
+    assert not wrong, wrong
+
+
 def test_gguf_fetch_needs_room_for_the_largest_record(qm, orc, tmp_path):
     """The fetch callback cannot be told the staging size.  The file's layers
     differ in down type (Q6_K, then Q4_K), so its records differ in size; a
@@ -280,6 +390,31 @@ def test_gguf_fetch_needs_room_for_the_largest_record(qm, orc, tmp_path):
         assert ok.get(1, 3) != 0 and ok.get(0, 3) != 0
     finally:
         ok.close()
+        g.close()
+
+
+def test_gguf_fetch_bound_spans_layer_gaps(qm, orc, tmp_path):
+    """A file whose expert layers have a gap (blk.0 and blk.2, no blk.1),
+    the later layer's record the larger (Q6_K down against Q4_K): a cache
+    sized for blk.0's record refuses the GGUF callback, since a fetch of
+    blk.2 would overrun its staging."""
+    N, F, E, K = 256, 256, 8, 2
+    l0 = make_host_layer(orc, seed=150, n_embd=N, n_ff=F, n_expert=E, n_used=K, t_down=12)
+    l2 = make_host_layer(orc, seed=152, n_embd=N, n_ff=F, n_expert=E, n_used=K, t_down=14)
+    t2 = [(n.replace("blk.0.", "blk.2."), ty, d, b) for n, ty, d, b in gw.moe_model_tensors([l2])]
+    path = tmp_path / "gap.gguf"
+    gw.write_gguf(path, gw.qwen35moe_metadata(3, N, E, K, F), gw.moe_model_tensors([l0]) + t2)
+    g = qm.Gguf(str(path))
+    small = 2 * F * (N // 256) * 144 + N * (F // 256) * 144
+    assert g.expert_record_bytes() == small + N * (F // 256) * (210 - 144)
+    c = qm.ECache(8 * small, small, fetch=qm.gguf_fetch_fn(), user=g.h)
+    try:
+        assert c.get(2, 1) == 0
+        with pytest.raises(qm.QmagError, match="largest"):
+            c.io_start(2, 2)
+        assert c.stats()["bytes_read"] == 0
+    finally:
+        c.close()
         g.close()
 
 

@@ -42,9 +42,12 @@ def run_layer(qm, rl, x, T):
     return ob.download(np.float32).reshape(T, rl.n_embd)
 
 
-def check_layer(qm, orc, rl, hl, x, T):
+def check_layer(qm, orc, rl, hl, x, T, run=None):
+    """Stage by stage against the oracle on hl's bytes.  `run(x, T)` computes
+    the layer on the device (default: qmag_moe_ffn_dev on rl) and leaves the
+    stage buffers of its last call for moe_last_stage."""
     N, F, E, K = hl.n_embd, hl.n_ff, hl.n_expert, hl.n_used
-    got = run_layer(qm, rl, x, T)
+    got = run(x, T) if run else run_layer(qm, rl, x, T)
     st = qm.moe_last_stage(E, K, F)
     # stage checks on token 0
     x0 = x[:N]
@@ -232,7 +235,7 @@ def test_moe_layer_prefill_skewed_router(qm, orc):
     rl.close()
 
 
-def check_layer_staged(qm, orc, rl, hl, x, T, stage1_tokens=None):
+def check_layer_staged(qm, orc, rl, hl, x, T, stage1_tokens=None, run=None):
     """All T tokens, stage by stage with teacher forcing (for batches, where
     many tokens are compared):
       1. logits, selection (outside near-ties), weights and shared gate
@@ -244,10 +247,11 @@ def check_layer_staged(qm, orc, rl, hl, x, T, stage1_tokens=None):
     Stage 3 starts from the GPU's h so that a last-bit difference in h --
     the fp32 epilogues are associated differently -- which moves one Q8_K(h)
     value by one step cannot fake or mask an error in the down projection;
-    stage 2 bounds that difference at the 1e-4 tolerance."""
+    stage 2 bounds that difference at the 1e-4 tolerance.  `run(x, T)`, if
+    given, computes the layer in place of qmag_moe_ffn_dev on rl."""
     N, F, E, K = hl.n_embd, hl.n_ff, hl.n_expert, hl.n_used
     S = K + 1
-    got = run_layer(qm, rl, x, T)
+    got = run(x, T) if run else run_layer(qm, rl, x, T)
     st = qm.moe_last_stage(E, K, F, n_tok=T)
     gb, db = hl.gate_exps.size // E, hl.down_exps.size // E
     tokens = range(T) if stage1_tokens is None else stage1_tokens
@@ -676,15 +680,17 @@ def test_stack_small_n_used(qm, orc, n_used):
         r.close()
 
 
-@pytest.mark.parametrize("case", ["nan_row", "inf_bias", "all_below_1e30"])
+@pytest.mark.parametrize("case", ["nan_row", "inf_bias", "all_below_1e30", "all_at_1e30"])
 @pytest.mark.parametrize("path", ["fused", "sequence", "grouped"])
 def test_route_degenerate_softmax(qm, orc, case, path):
     """When the reference's softmax is NaN throughout -- a NaN logit, a +Inf
-    logit, or every logit at or below its -1e30 starting maximum -- its top-K
-    scan picks expert 0 for every slot with weight -1e30 / (K * -1e30)
-    (nn.c:517-536).  Every GPU path makes the same picks and weights, and the
-    output (expert 0 eight times plus the shared expert) matches the oracle
-    stage by stage."""
+    logit, or every logit strictly below its -1e30 starting maximum -- its
+    top-K scan picks expert 0 for every slot with weight -1e30 / (K * -1e30)
+    (nn.c:517-536).  Every logit at exactly -1e30 is not degenerate: the
+    maximum stays at -1e30, every term is expf(0) = 1 and the scan picks
+    experts 0..K-1 (equal probabilities, lowest index first) with weight 1/K.
+    Every GPU path makes the same picks and weights, and the output matches
+    the oracle stage by stage."""
     E, K, N, F = 32, 8, 2048, 512
     hl = make_host_layer(orc, seed=88, n_embd=N, n_ff=F, n_expert=E, n_used=K, router_bias_std=0.0)
     wr = hl.gate_inp.reshape(E, N)
@@ -693,8 +699,10 @@ def test_route_degenerate_softmax(qm, orc, case, path):
         wr[5, 100] = np.nan
     elif case == "inf_bias":
         bias[9] = np.inf
-    else:
+    elif case == "all_below_1e30":
         bias[:] = -2e30
+    else:
+        bias[:] = -1e30            # the dot (|.| ~ 1) is absorbed: every logit is exactly -1e30
     rl = qm.ResidentLayer.from_host(hl)
     T = 16 if path == "grouped" else 1
     x = orc.fill_normal(19, T * N, 0.0, 1.0)
@@ -708,16 +716,18 @@ def test_route_degenerate_softmax(qm, orc, case, path):
     for t in range(T):
         xt = x[t * N:(t + 1) * N]
         sel_o, w_o, _ = orc.moe_route(hl, xt)
-        assert list(sel_o) == [0] * K
+        assert list(sel_o) == (list(range(K)) if case == "all_at_1e30" else [0] * K)
         assert list(st["sel"][t]) == list(sel_o), f"token {t}"
         assert np.array_equal(st["w"][t].view(np.uint32), w_o.view(np.uint32)), f"token {t}"
         xq, xd, xs = orc.q8k_quant(xt)
-        h0 = orc.moe_expert_h(hl.gate_exps[:gb], hl.up_exps[:gb], N, F, xq, xd, xs)
         acc = np.zeros(N, np.float32)
         for s in range(K + 1):
             if s < K:
-                assert max_rel_err(st["h"][t][s], h0) < TOL
-                dn, scale = hl.down_exps[:db], st["w"][t][s]
+                e = int(sel_o[s])
+                h = orc.moe_expert_h(hl.gate_exps[e * gb:(e + 1) * gb], hl.up_exps[e * gb:(e + 1) * gb],
+                                     N, F, xq, xd, xs)
+                assert max_rel_err(st["h"][t][s], h) < TOL
+                dn, scale = hl.down_exps[e * db:(e + 1) * db], st["w"][t][s]
             else:
                 dn, scale = hl.down_shexp, st["gs"][t]
             y = orc.matmul_q8k(st["h"][t][s], dn, F, N, 1, hl.t_down_exps)[0]

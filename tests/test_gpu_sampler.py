@@ -150,3 +150,30 @@ def test_sample_all_masked(qm, orc):
     d = qm.DBuf.from_array(np.full(5000, -1e30, np.float32))
     assert qm.sampler_sample_dev(d.ptr, 5000, sd, 40, 0.95) == 0
     assert sd.seed == 9 and sd.n_last == 0
+
+
+def test_sample_after_recovery_reports_stale_logits(qm, orc):
+    """A persistent decode launch queued before the sampler finds its abort
+    word set (the test hook, as after an expired wait).  The sampler's status
+    check re-runs that call, but the logits were meant to come from its
+    output, so the sampler samples nothing, leaves the state unchanged and
+    returns QMAG_ERR_REPLAYED; called again, it samples as the oracle does."""
+    rl = qm.ResidentLayer(seed=3, layer=0)
+    x = qm.DBuf.from_array(orc.fill_normal(12, 2048, 0.0, 1.0))
+    out = qm.DBuf(4 * 2048)
+    logits = (np.random.default_rng(41).standard_normal(5000) * 2.5).astype(np.float32)
+    d = qm.DBuf.from_array(logits)
+    kw = dict(seed=777, temp=0.8, top_k=20, top_p=0.9, repeat_penalty=1.0)
+    sd, so = _state(qm, orc, **kw)
+    r0 = qm.fused_recoveries()
+    qm.arm_test_abort(1)
+    qm.moe_ffn_dev(rl.c, x.ptr, out.ptr, 1)
+    with pytest.raises(qm.QmagError, match="status -5"):
+        qm.sampler_sample_dev(d.ptr, logits.size, sd, 40, 0.9)
+    assert qm.fused_recoveries() == r0 + 1
+    assert sd.seed == 777 and sd.n_last == 0
+    gt = qm.sampler_sample_dev(d.ptr, logits.size, sd, 40, 0.9)
+    oi, ov = orc.sampler_candidates(logits, so, 40)
+    assert gt == orc.sampler_pick(so, oi, ov, 0.9)
+    assert sd.seed == so.seed and sd.n_last == so.n_last == 1
+    rl.close()

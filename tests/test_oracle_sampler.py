@@ -104,3 +104,63 @@ def test_draw_is_uniform(orc):
         s.n_last = 0
     chi2 = float(np.sum((c - 5000) ** 2 / 5000))
     assert chi2 < 30.0, c
+
+
+M64 = (1 << 64) - 1
+
+
+def _xorshift64star(state, shifts=(12, 25, 27), mult=0x2545F4914F6CDD1D):
+    """One step of xorshift64* as published (S. Vigna, "An experimental
+    exploration of Marsaglia's xorshift generators, scrambled", ACM TOMS 42(4),
+    2016): x ^= x >> 12; x ^= x << 25; x ^= x >> 27; output x * M mod 2^64.
+    Written here from that description, not from the oracle; `shifts` and
+    `mult` let the test plant the plausible mistakes below."""
+    a, b, c = shifts
+    x = state
+    x ^= x >> a
+    x = (x ^ (x << b)) & M64
+    x ^= x >> c
+    return x, (x * mult) & M64
+
+
+def _kat(seed, steps, **kw):
+    """States after each step and the pick each draw makes over 1024 equal
+    candidates: rv = float32((r >> 11) / 2^53) and the cumulative sums k/1024
+    are exact in float32, so the pick is floor(rv * 1024)."""
+    states, picks, x = [], [], seed
+    for _ in range(steps):
+        x, r = _xorshift64star(x, **kw)
+        rv = np.float32((r >> 11) * (1.0 / 9007199254740992.0))
+        states.append(x)
+        picks.append(int(np.floor(np.float64(rv) * 1024)))
+    return states, picks
+
+
+@pytest.mark.parametrize("seed", [1, 12345, 0x9E3779B97F4A7C15, 0xDEADBEEFCAFEF00D])
+def test_rng_known_answers(orc, seed):
+    """The oracle's draw (orc_rng_next, sampler.c:9-14, and the (r >> 11) / 2^53
+    uniform of sampler.c:118) against xorshift64* from its publication: the
+    state after every draw and every pick over 1024 equal candidates agree for
+    32 draws.  The plausible mistakes -- the 25/27 shifts swapped, a left shift
+    first, the multiplier's last digit changed, the uniform taken from r >> 12
+    -- each give other states or picks, so this check tells them apart."""
+    steps = 32
+    s = orc.make_sampler(temp=1.0, seed=seed)
+    ids = np.arange(1024, dtype=np.int32)
+    got_states, got_picks = [], []
+    for _ in range(steps):
+        got_picks.append(orc.sampler_pick(s, ids, np.zeros(1024, np.float32), 1.0))
+        got_states.append(int(s.seed))
+        s.n_last = 0
+    want_states, want_picks = _kat(seed, steps)
+    assert got_states == want_states
+    assert got_picks == want_picks
+    for wrong in (dict(shifts=(12, 27, 25)), dict(shifts=(25, 12, 27)), dict(mult=0x2545F4914F6CDD1C)):
+        ws, wp = _kat(seed, steps, **wrong)
+        assert ws != got_states or wp != got_picks, wrong
+    # the uniform from r >> 12 instead of r >> 11 halves rv: other picks
+    x, wrong_picks = seed, []
+    for _ in range(steps):
+        x, r = _xorshift64star(x)
+        wrong_picks.append(int(np.floor(np.float64(np.float32((r >> 12) * (1.0 / 9007199254740992.0))) * 1024)))
+    assert wrong_picks != got_picks
