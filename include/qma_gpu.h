@@ -268,6 +268,15 @@ typedef struct qmag_moe_layer {
    sigmoid(gs) * shared(x[t]) for T tokens (x, out: f32 [T][n_embd]). */
 int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *out, int T);
 
+/* The moe_ffn seam with q8k off (QMA_NOQ8K, or no q8k; nn.c:585): the same
+   routing, then moe_expert_one and moe_shared (nn.c:393-407, 475-492) --
+   expert h on fp32 x, the shared gate sigmoid(wsh . x) on fp32 x, every dot
+   dequantise-then-dot in fp32 -- and the combine in the reference's order.
+   Replaces the per-row dot_q4_K_f32 / dot_q6_K_f32 calls of that path with
+   three launches per call.  Same shapes and stage buffers
+   (qmag_moe_last_stage) as qmag_moe_ffn_dev; T <= 65535. */
+int qmag_moe_ffn_f32_dev(const qmag_moe_layer *L, const float *x, float *out, int T);
+
 /* Decode over a stack of MoE layers: for each of n_tok tokens in turn,
    x[t] <- x[t] + moe_l(x[t]) for l = 0..n_layer-1 (the residual add of
    qma_eval, nn.c:2252).  x: f32 [n_tok][n_embd], updated in place.  Layers

@@ -73,6 +73,10 @@ def _declare(L):
     L.orc_moe_shared_gate.restype = C.c_float
     L.orc_moe_shared_gate.argtypes = [P, P, P, C.c_int]
     L.orc_moe_stack.argtypes = [C.POINTER(MoeLayer), C.c_int, P]
+    L.orc_moe_expert_h_f32.argtypes = [P, P, C.c_int, C.c_int, P, P]
+    L.orc_moe_shared_gate_f32.restype = C.c_float
+    L.orc_moe_shared_gate_f32.argtypes = [P, P, C.c_int]
+    L.orc_moe_ffn_f32.argtypes = [C.POINTER(MoeLayer), P, P, C.c_int]
     L.orc_fill_normal.argtypes = [C.c_uint64, C.c_int64, C.c_float, C.c_float, P]
     L.orc_sampler_candidates.restype = C.c_int
     L.orc_sampler_candidates.argtypes = [C.c_int, P, C.POINTER(Sampler), P, P, C.c_int]
@@ -336,6 +340,23 @@ def moe_expert_h(ge, ue, n_embd, n_ff, xq, xd, xs):
     h = np.empty(n_ff, dtype=np.float32)
     lib().orc_moe_expert_h(_p(ge), _p(ue), n_embd, n_ff, _p(xq), _p(xd), _p(xs), _p(h))
     return h
+
+
+def moe_ffn_f32(layer: HostLayer, x: np.ndarray, T: int) -> np.ndarray:
+    """The fp32 twin of moe_ffn (QMA_NOQ8K)."""
+    out = np.empty(T * layer.n_embd, dtype=np.float32)
+    lib().orc_moe_ffn_f32(C.byref(layer.c), _p(np.ascontiguousarray(x, dtype=np.float32)), _p(out), T)
+    return out.reshape(T, layer.n_embd)
+
+
+def moe_expert_h_f32(ge, ue, n_embd, n_ff, x):
+    h = np.empty(n_ff, dtype=np.float32)
+    lib().orc_moe_expert_h_f32(_p(ge), _p(ue), n_embd, n_ff, _p(np.ascontiguousarray(x, dtype=np.float32)), _p(h))
+    return h
+
+
+def moe_shared_gate_f32(wsh, x, n_embd) -> float:
+    return float(lib().orc_moe_shared_gate_f32(_p(wsh), _p(np.ascontiguousarray(x, dtype=np.float32)), n_embd))
 
 
 def moe_shared_gate(wsh, xq, xd, n_embd) -> float:

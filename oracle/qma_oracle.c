@@ -737,6 +737,77 @@ void orc_moe_ffn(const orc_moe_layer *L, const float *x, float *out, int T)
     free(w);
 }
 
+/* ---- the fp32 twins, taken when QMA_NOQ8K is set or q8k is unavailable
+   (nn.c:585): no activation quantisation, dequantise-then-dot throughout. */
+
+/* h = silu(gate . x) * (up . x) on fp32 x, the first loop of moe_expert_one
+   (nn.c:395-400) and of moe_shared (nn.c:480-484). */
+void orc_moe_expert_h_f32(const uint8_t *ge, const uint8_t *ue, int n_embd, int n_ff, const float *x,
+                          float *h)
+{
+    const size_t gu_row = q4k_row_bytes(n_embd);
+    for (int i = 0; i < n_ff; i++) {
+        const float g = orc_dot_q4k_f32(ge + (size_t)i * gu_row, x, n_embd);
+        const float u = orc_dot_q4k_f32(ue + (size_t)i * gu_row, x, n_embd);
+        h[i] = (g / (1.0f + expf(-g))) * u;
+    }
+}
+
+/* acc[i] += we * down_i . h over fp32 h (nn.c:401-406, 485-490) */
+static void down_f32(const uint8_t *de, int de_type, int n_embd, int n_ff, const float *h, float we,
+                     float *acc)
+{
+    const size_t dn_row = row_bytes(n_ff, de_type);
+    for (int i = 0; i < n_embd; i++) {
+        const float y = de_type == ORC_TYPE_Q4_K ? orc_dot_q4k_f32(de + (size_t)i * dn_row, h, n_ff)
+                                                 : orc_dot_q6k_f32(de + (size_t)i * dn_row, h, n_ff);
+        acc[i] += we * y;
+    }
+}
+
+/* the shared gate of moe_shared (nn.c:477-479): fp32 x, serial sum, sigmoid */
+float orc_moe_shared_gate_f32(const float *wsh, const float *x, int n_embd)
+{
+    float gs = 0;
+    for (int i = 0; i < n_embd; i++) gs += wsh[i] * x[i];
+    return 1.0f / (1.0f + expf(-gs));
+}
+
+/* moe_ffn with q8k off (nn.c:576-629): the router as in the q8k branch, one
+   moe_expert_one per (token, slot) into a zeroed partial, the partials
+   summed in slot order, then moe_shared added. */
+void orc_moe_ffn_f32(const orc_moe_layer *L, const float *x, float *out, int T)
+{
+    const int N = L->n_embd, F = L->n_ff, K = L->n_used;
+    const size_t ge_bytes = (size_t)F * q4k_row_bytes(N);
+    const size_t dn = (size_t)N * row_bytes(F, L->t_down_exps);
+    int *sel = (int *)malloc(sizeof(int) * (size_t)K);
+    float *w = (float *)malloc(sizeof(float) * (size_t)K);
+    float *h = (float *)malloc(sizeof(float) * (size_t)F);
+    float *part = (float *)malloc(sizeof(float) * (size_t)N);
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * N;
+        float *acc = out + (size_t)t * N;
+        orc_moe_route(L, xt, sel, w, NULL);
+        memset(acc, 0, sizeof(float) * (size_t)N);
+        for (int k = 0; k < K; k++) {
+            const int ex = sel[k];
+            orc_moe_expert_h_f32(L->gate_exps + (size_t)ex * ge_bytes, L->up_exps + (size_t)ex * ge_bytes, N, F,
+                                 xt, h);
+            memset(part, 0, sizeof(float) * (size_t)N);
+            down_f32(L->down_exps + (size_t)ex * dn, L->t_down_exps, N, F, h, w[k], part);
+            for (int i = 0; i < N; i++) acc[i] += part[i];
+        }
+        const float gs = orc_moe_shared_gate_f32(L->gate_inp_shexp, xt, N);
+        orc_moe_expert_h_f32(L->gate_shexp, L->up_shexp, N, F, xt, h);
+        down_f32(L->down_shexp, L->t_down_shexp, N, F, h, gs, acc);
+    }
+    free(sel);
+    free(w);
+    free(h);
+    free(part);
+}
+
 /* Layer stack of the decode workload: x <- moe_l(x) + x for each layer, the
    residual add of qma_eval (nn.c:2252) with the non-FFN parts of the layer
    left out. */

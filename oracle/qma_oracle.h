@@ -111,6 +111,12 @@ void     orc_moe_expert_h(const uint8_t *ge, const uint8_t *ue, int n_embd,
                           const int16_t *xsum, float *h);
 float    orc_moe_shared_gate(const float *wsh, const int8_t *xq,
                              const float *xd, int n_embd);
+/* fp32 twins (QMA_NOQ8K, nn.c:393-407, 475-492, 585): no activation
+   quantisation; expert h on fp32 x, the fp32 shared gate, the full layer */
+void     orc_moe_expert_h_f32(const uint8_t *ge, const uint8_t *ue, int n_embd,
+                              int n_ff, const float *x, float *h);
+float    orc_moe_shared_gate_f32(const float *wsh, const float *x, int n_embd);
+void     orc_moe_ffn_f32(const orc_moe_layer *L, const float *x, float *out, int T);
 /* residual chain used by the layer-stack workload: x <- x + moe_l(x) */
 void     orc_moe_stack(const orc_moe_layer *layers, int n_layer, float *x);
 

@@ -416,6 +416,67 @@ __device__ __forceinline__ int q6_int_dot(const Q6Raw &r, const Q6Act &a, int l1
     return tot;
 }
 
+// ------------------------------------------------ fp32 dequant-dot ----
+// One 64-value task of an fp32 dot deq(row) . x (quants.c:80-133): Q4_K task
+// t covers the nibble group t & 3 of super-block t >> 2 (its 16-byte header
+// and 32 bytes of nibbles), Q6_K task t a quarter of super-block t >> 2.  xs
+// is the fp32 operand (in LDS).  The tasks of a row summed in any order give
+// the row's dot to fp32 rounding.
+template <int WT>
+__device__ __forceinline__ float f32_task(const uint8_t *row, int t, const float *xs)
+{
+    const int ib = t >> 2, q = t & 3;
+    if constexpr (WT == QMAG_TYPE_Q4_K) {
+        const uint8_t *b = row + (size_t)ib * Q4K_BYTES;
+        const uint4 hdr = ld16(b), q0 = ld16(b + 16 + 32 * q), q1 = ld16(b + 32 + 32 * q);
+        const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
+        uint32_t s1, m1, s2, m2;
+        q4_scale_min(2 * q, hdr.y, hdr.z, hdr.w, s1, m1);
+        q4_scale_min(2 * q + 1, hdr.y, hdr.z, hdr.w, s2, m2);
+        const float d1 = d * (float)s1, dm1 = dmin * (float)m1;
+        const float d2 = d * (float)s2, dm2 = dmin * (float)m2;
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const float4 *xv = (const float4 *)(xs + ib * QK_K + 64 * q);
+        float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 a = xv[k], c = xv[8 + k];
+            const uint32_t w = qw[k];
+            lo += (d1 * (float)(w & 15) - dm1) * a.x + (d1 * (float)((w >> 8) & 15) - dm1) * a.y +
+                  (d1 * (float)((w >> 16) & 15) - dm1) * a.z + (d1 * (float)((w >> 24) & 15) - dm1) * a.w;
+            hi += (d2 * (float)((w >> 4) & 15) - dm2) * c.x + (d2 * (float)((w >> 12) & 15) - dm2) * c.y +
+                  (d2 * (float)((w >> 20) & 15) - dm2) * c.z + (d2 * (float)((w >> 28) & 15) - dm2) * c.w;
+        }
+        return lo + hi;
+    } else {
+        const uint8_t *b = row + (size_t)ib * Q6K_BYTES;
+        const int n = q >> 1, l16 = q & 1;
+        Q6Raw r;
+        q6_load_raw(r, b, n, l16);
+        const float d = h2f(r.d);
+        const uint64_t sc8 = ((uint64_t)r.sc.y << 32) | r.sc.x;
+        const uint32_t L[4] = {r.ql_lo.x, r.ql_lo.y, r.ql_lo.z, r.ql_lo.w};
+        const uint32_t H[4] = {r.ql_hi.x, r.ql_hi.y, r.ql_hi.z, r.ql_hi.w};
+        const uint32_t B[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        float acc = 0.0f;
+#pragma unroll
+        for (int Q = 0; Q < 4; Q++) {
+            const float ds = d * (float)(int)(int8_t)((sc8 >> (8 * (l16 + 2 * Q))) & 255);
+            const float4 *xv = (const float4 *)(xs + ib * QK_K + 128 * n + 32 * Q + 16 * l16);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t src = (Q & 1) ? H[k] : L[k];
+                const uint32_t lo = (Q >= 2 ? src >> 4 : src) & 0x0F0F0F0Fu;
+                const uint32_t qv = lo | (((B[k] >> (2 * Q)) & 0x03030303u) << 4);
+                const float4 a = xv[k];
+                acc += ds * (float)((int)(qv & 255) - 32) * a.x + ds * (float)((int)((qv >> 8) & 255) - 32) * a.y +
+                       ds * (float)((int)((qv >> 16) & 255) - 32) * a.z + ds * (float)((int)(qv >> 24) - 32) * a.w;
+            }
+        }
+        return acc;
+    }
+}
+
 // ---------------------------------------------------------- routing ----
 // The reference's softmax (nn.c:517-527) turns every probability into NaN
 // when one logit is NaN or +Inf (its term is NaN), or when every logit is

@@ -686,7 +686,11 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 ok = read_logits(E, seq, lg);
                 int my_sel = 0;
                 float my_w = 0.0f;
+                // the picks are a chain of dependent wave reductions: issue
+                // them ahead of the other wave sharing this SIMD
+                __builtin_amdgcn_s_setprio(3);
                 route_topk(lg, E, K, my_sel, my_w);
+                __builtin_amdgcn_s_setprio(0);
                 if (lane < K) {
                     s_sel[lane] = my_sel;
                     s_w[lane] = my_w;
@@ -790,7 +794,9 @@ __global__ __launch_bounds__(256, 2) void moe_decode_kernel(const qmag_moe_layer
                 TR(7);
                 int my_sel = 0;
                 float my_w = 0.0f;
+                __builtin_amdgcn_s_setprio(3);        // as in the core workgroups
                 route_topk(lg, E, K, my_sel, my_w);
+                __builtin_amdgcn_s_setprio(0);
                 if (lane < K) s_sel[lane] = my_sel;
                 TR(6);
             } else if (wv >= 2) {

@@ -377,6 +377,111 @@ __global__ __launch_bounds__(256) void down_kernel(const uint8_t *__restrict__ d
 }
 
 // ------------------------------------------------------------------ host --
+// -------------------------------------------- fp32 twins (QMA_NOQ8K) --
+// moe_expert_one and moe_shared (nn.c:393-407, 475-492), which the reference
+// takes when QMA_NOQ8K is set or q8k is unavailable (nn.c:585): no
+// activation quantisation, every dot dequantise-then-dot in fp32 (f32_task).
+// Routing is the q8k branch's (router_kernel, topk_kernel).
+constexpr int F32_MAX_N = 4096, F32_MAX_SF = 9 * 1024;   // n_embd; (n_used + 1) * n_ff
+
+// h[t][s][i] = silu(gate_i . x[t]) * (up_i . x[t]) for slot s (s < K: expert
+// sel[t][s]; s = K: the shared expert).  Grid (row blocks, K + 1, T); LPR
+// lanes per row.  Workgroup (0, K, t) also writes the fp32 shared gate
+// sigmoid(wsh . x[t]) (nn.c:477-479) to gs[t].
+template <int LPR>
+__global__ __launch_bounds__(256) void moe_f32_gateup_kernel(const uint8_t *__restrict__ gate_exps,
+                                                             const uint8_t *__restrict__ up_exps,
+                                                             const uint8_t *__restrict__ gate_shexp,
+                                                             const uint8_t *__restrict__ up_shexp,
+                                                             const float *__restrict__ wsh,
+                                                             const int *__restrict__ sel, int K, int N, int F,
+                                                             const float *__restrict__ x, float *__restrict__ h,
+                                                             float *__restrict__ gs)
+{
+    __shared__ __align__(16) float s_x[F32_MAX_N];
+    const int t = (int)blockIdx.z, s = (int)blockIdx.y, S = K + 1;
+    for (int i = (int)threadIdx.x; i < N / 4; i += (int)blockDim.x)
+        ((float4 *)s_x)[i] = ldg4(x + (size_t)t * N + 4 * i);
+    __syncthreads();
+    const int nb = N / QK_K, ntask = 4 * nb;
+    const size_t rb = (size_t)nb * Q4K_BYTES, slab = (size_t)F * rb;
+    const uint8_t *ge = s < K ? gate_exps + (size_t)sel[(size_t)t * K + s] * slab : gate_shexp;
+    const uint8_t *ue = s < K ? up_exps + (size_t)sel[(size_t)t * K + s] * slab : up_shexp;
+    const int lane = lane_id(), wave = (int)(threadIdx.x >> 6), sub = lane % LPR;
+    const int row = ((int)blockIdx.x * 4 + wave) * (64 / LPR) + lane / LPR;
+    float g = 0.0f, u = 0.0f;
+    if (row < F)
+        for (int tk = sub; tk < ntask; tk += LPR) {
+            g += f32_task<QMAG_TYPE_Q4_K>(ge + (size_t)row * rb, tk, s_x);
+            u += f32_task<QMAG_TYPE_Q4_K>(ue + (size_t)row * rb, tk, s_x);
+        }
+    g = group_sum<LPR>(g);
+    u = group_sum<LPR>(u);
+    if (sub == 0 && row < F) h[((size_t)t * S + s) * F + row] = (g / (1.0f + expf(-g))) * u;
+    if (blockIdx.x == 0 && s == K && wave == 0) {
+        float v = 0.0f;
+        for (int i = lane; i < N; i += 64) v += wsh[i] * s_x[i];
+        v = group_sum<64>(v);
+        if (lane == 0) gs[t] = 1.0f / (1.0f + expf(-v));
+    }
+}
+
+// out[t][r] = sum_k w_k * (down_k[r] . h_k) + gs * (down_sh[r] . h_sh), the
+// partials summed in the reference's order (slots 0..K-1, then the shared
+// expert; nn.c:614-629), products and sums separately rounded.  Grid (row
+// blocks, T); the token's K + 1 h vectors in LDS.
+template <int LPR, int TD, int TDS>
+__global__ __launch_bounds__(256) void moe_f32_down_kernel(const uint8_t *__restrict__ down_exps,
+                                                           const uint8_t *__restrict__ down_shexp,
+                                                           const int *__restrict__ sel, const float *__restrict__ w,
+                                                           const float *__restrict__ gs, int K, int N, int F,
+                                                           const float *__restrict__ h, float *__restrict__ out)
+{
+    __shared__ __align__(16) float s_h[F32_MAX_SF];
+    const int t = (int)blockIdx.y, S = K + 1;
+    for (int i = (int)threadIdx.x; i < S * F / 4; i += (int)blockDim.x)
+        ((float4 *)s_h)[i] = ldg4(h + (size_t)t * S * F + 4 * i);
+    __syncthreads();
+    const int nb = F / QK_K, ntask = 4 * nb;
+    const size_t rb = (size_t)nb * (TD == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES), slab = (size_t)N * rb;
+    const size_t rbs = (size_t)nb * (TDS == QMAG_TYPE_Q6_K ? Q6K_BYTES : Q4K_BYTES);
+    const int lane = lane_id(), wave = (int)(threadIdx.x >> 6), sub = lane % LPR;
+    const int row = ((int)blockIdx.x * 4 + wave) * (64 / LPR) + lane / LPR;
+    const bool live = row < N;
+    float acc = 0.0f;
+    for (int k = 0; k < K; k++) {
+        const uint8_t *dr = down_exps + (size_t)sel[(size_t)t * K + k] * slab + (size_t)(live ? row : 0) * rb;
+        float y = 0.0f;
+        if (live)
+            for (int tk = sub; tk < ntask; tk += LPR) y += f32_task<TD>(dr, tk, s_h + k * F);
+        y = group_sum<LPR>(y);
+        acc = __fadd_rn(acc, __fmul_rn(w[(size_t)t * K + k], y));
+    }
+    float y = 0.0f;
+    if (live)
+        for (int tk = sub; tk < ntask; tk += LPR) y += f32_task<TDS>(down_shexp + (size_t)row * rbs, tk, s_h + K * F);
+    y = group_sum<LPR>(y);
+    acc = __fadd_rn(acc, __fmul_rn(gs[t], y));
+    if (sub == 0 && live) out[(size_t)t * N + row] = acc;
+}
+
+template <int TD, int TDS>
+static void launch_f32_down(const qmag_moe_layer *L, const int *sel, const float *w, const float *gs,
+                            const float *h, float *out, int T, hipStream_t s)
+{
+    const int N = L->n_embd, F = L->n_ff, K = L->n_used;
+    const int ntask = 4 * (F / QK_K);
+    const uint8_t *de = (const uint8_t *)L->down_exps, *ds = (const uint8_t *)L->down_shexp;
+    switch (ntask) {
+    case 4: hipLaunchKernelGGL((moe_f32_down_kernel<4, TD, TDS>), dim3((N + 63) / 64, T), dim3(256), 0, s, de, ds,
+                               sel, w, gs, K, N, F, h, out); break;
+    case 8: hipLaunchKernelGGL((moe_f32_down_kernel<8, TD, TDS>), dim3((N + 31) / 32, T), dim3(256), 0, s, de, ds,
+                               sel, w, gs, K, N, F, h, out); break;
+    default: hipLaunchKernelGGL((moe_f32_down_kernel<16, TD, TDS>), dim3((N + 15) / 16, T), dim3(256), 0, s, de,
+                                ds, sel, w, gs, K, N, F, h, out); break;
+    }
+}
+
 static bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
 
 // batches of at least this many tokens take the grouped expert GEMM
@@ -676,6 +781,51 @@ extern "C" int qmag_moe_ffn_paged_dev(const qmag_moe_layer *L, qmag_ecache *c, i
         qmag_ecache_release(c);      // after the launches: later copies wait for them
         if (st) return st;
     }
+    QMAG_HIP(hipGetLastError());
+    g_last = ws;
+    g_last_K = K;
+    return QMAG_OK;
+}
+
+// the QMA_NOQ8K layer (nn.c:585): the q8k branch's routing, then the fp32
+// expert stages; the stage buffers hold its logits, selection, weights,
+// fp32 shared gate and fp32 h
+extern "C" int qmag_moe_ffn_f32_dev(const qmag_moe_layer *L, const float *x, float *out, int T)
+{
+    int st = require_ready();
+    if (st) return st;
+    st = moe_check_layer(L);
+    if (st) return st;
+    if (T <= 0 || T > 65535 || !x || !out) return fail(QMAG_ERR_ARG, "moe_f32: T=%d x=%p out=%p", T, x, out);
+    const int N = L->n_embd, F = L->n_ff, K = L->n_used, S = K + 1;
+    if (N > F32_MAX_N || S * F > F32_MAX_SF) return fail(QMAG_ERR_ARG, "moe_f32: n_embd=%d n_ff=%d", N, F);
+    hipStream_t s = ctx().stream;
+    MoeWs ws;
+    st = moe_ws(L, T, ws);
+    if (st) return st;
+    g_last_fused = false;
+    st = route_tokens(L, x, T, false, ws, s);
+    if (st) return st;
+    const int ntask = 4 * (N / QK_K);
+    const dim3 gu_grid((unsigned)((F + 15) / 16), (unsigned)S, (unsigned)T);
+    const uint8_t *ge = (const uint8_t *)L->gate_exps, *ue = (const uint8_t *)L->up_exps;
+    const uint8_t *gsh = (const uint8_t *)L->gate_shexp, *ush = (const uint8_t *)L->up_shexp;
+    prof_begin(PROF_GATEUP, s);
+    if (ntask >= 32) {
+        hipLaunchKernelGGL(moe_f32_gateup_kernel<32>, dim3((F + 7) / 8, S, T), dim3(256), 0, s, ge, ue, gsh, ush,
+                           L->gate_inp_shexp, ws.sel, K, N, F, x, ws.h, ws.gs);
+    } else {
+        hipLaunchKernelGGL(moe_f32_gateup_kernel<16>, gu_grid, dim3(256), 0, s, ge, ue, gsh, ush, L->gate_inp_shexp,
+                           ws.sel, K, N, F, x, ws.h, ws.gs);
+    }
+    prof_end(PROF_GATEUP, s);
+    prof_begin(PROF_DOWN, s);
+    const bool r6 = L->t_down_exps == QMAG_TYPE_Q6_K, s6 = L->t_down_shexp == QMAG_TYPE_Q6_K;
+    if (r6 && s6) launch_f32_down<QMAG_TYPE_Q6_K, QMAG_TYPE_Q6_K>(L, ws.sel, ws.w, ws.gs, ws.h, out, T, s);
+    else if (r6) launch_f32_down<QMAG_TYPE_Q6_K, QMAG_TYPE_Q4_K>(L, ws.sel, ws.w, ws.gs, ws.h, out, T, s);
+    else if (s6) launch_f32_down<QMAG_TYPE_Q4_K, QMAG_TYPE_Q6_K>(L, ws.sel, ws.w, ws.gs, ws.h, out, T, s);
+    else launch_f32_down<QMAG_TYPE_Q4_K, QMAG_TYPE_Q4_K>(L, ws.sel, ws.w, ws.gs, ws.h, out, T, s);
+    prof_end(PROF_DOWN, s);
     QMAG_HIP(hipGetLastError());
     g_last = ws;
     g_last_K = K;

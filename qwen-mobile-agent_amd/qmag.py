@@ -59,6 +59,7 @@ SIGNATURES = {
     "qmag_dequant_dev": (C.c_int, [P, C.c_int, C.c_int64, P]),
     "qmag_matmul_f32_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_moe_ffn_dev": (C.c_int, [P, P, P, C.c_int]),
+    "qmag_moe_ffn_f32_dev": (C.c_int, [P, P, P, C.c_int]),
     "qmag_moe_stack_dev": (C.c_int, [P, C.c_int, P, C.c_int]),
     "qmag_moe_last_stage": (C.c_int, [C.POINTER(P)] * 5),
     "qmag_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
@@ -295,6 +296,11 @@ def matmul_f32_dev(x: DBuf, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> None:
 
 def moe_ffn_dev(layer: MoeLayer, x_ptr: int, out_ptr: int, T: int) -> None:
     check(lib().qmag_moe_ffn_dev(C.byref(layer), x_ptr, out_ptr, T))
+
+
+def moe_ffn_f32_dev(layer: MoeLayer, x_ptr: int, out_ptr: int, T: int) -> None:
+    """The fp32 twin of the layer (QMA_NOQ8K)."""
+    check(lib().qmag_moe_ffn_f32_dev(C.byref(layer), x_ptr, out_ptr, T))
 
 
 def moe_stack_dev(layers, x_ptr: int, n_tok: int) -> None:

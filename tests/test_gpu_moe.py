@@ -734,3 +734,50 @@ def test_route_degenerate_softmax(qm, orc, case, path):
             acc = (acc + (np.float32(scale) * y).astype(np.float32)).astype(np.float32)
         assert max_rel_err(got[t], acc) < TOL, f"output, token {t}"
     rl.close()
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(n_embd=512, n_ff=256, n_expert=16, n_used=4, t_down=14),
+    dict(n_embd=2048, n_ff=512, n_expert=32, n_used=8, t_down=12),
+    dict(n_embd=1024, n_ff=1024, n_expert=64, n_used=6, t_down=14),
+    dict(n_embd=4096, n_ff=256, n_expert=16, n_used=8, t_down=12),
+])
+def test_moe_layer_f32_vs_oracle(qm, orc, cfg):
+    """qmag_moe_ffn_f32_dev, the QMA_NOQ8K layer (nn.c:393-407, 475-492, 585),
+    against orc_moe_ffn_f32 on the same bytes, stage by stage: the router as
+    the q8k branch's, the fp32 shared gate on fp32 x, h of every slot (fp32
+    dequantise-then-dot, 1e-4 of max|h|) and the output (1e-4 of max|y|; no
+    activation is requantised on this path, so the output is compared whole)
+    for every token whose selection is not a near-tie."""
+    hl = make_host_layer(orc, seed=31, **cfg)
+    rl = qm.ResidentLayer.from_host(hl)
+    N, F, E, K = hl.n_embd, hl.n_ff, hl.n_expert, hl.n_used
+    gb = hl.gate_exps.size // E
+    for T in (1, 5):
+        x = orc.fill_normal(60 + T, T * N, 0.0, 1.0)
+        xb = qm.DBuf.from_array(x)
+        ob = qm.DBuf(4 * T * N)
+        qm.moe_ffn_f32_dev(rl.c, xb.ptr, ob.ptr, T)
+        got = ob.download(np.float32).reshape(T, N)
+        st = qm.moe_last_stage(E, K, F, n_tok=T)
+        ref = orc.moe_ffn_f32(hl, x, T)
+        compared = 0
+        for t in range(T):
+            xt = x[t * N:(t + 1) * N]
+            sel_o, w_o, lg_o = orc.moe_route(hl, xt)
+            assert max_rel_err(st["logits"][t], lg_o) < TOL, f"logits, token {t}"
+            assert abs(st["gs"][t] - orc.moe_shared_gate_f32(hl.gate_inp_shexp, xt, N)) < 1e-6
+            for s in range(K + 1):
+                if s < K:
+                    e = int(st["sel"][t][s])
+                    ge, ue = hl.gate_exps[e * gb:(e + 1) * gb], hl.up_exps[e * gb:(e + 1) * gb]
+                else:
+                    ge, ue = hl.gate_shexp, hl.up_shexp
+                h = orc.moe_expert_h_f32(ge, ue, N, F, xt)
+                assert max_rel_err(st["h"][t][s], h) < TOL, f"h, token {t} slot {s}"
+            if route_margin(lg_o, K) > TIE:
+                assert list(st["sel"][t]) == list(sel_o), f"selection, token {t}"
+                assert max_rel_err(got[t], ref[t]) < TOL, f"output, token {t}"
+                compared += 1
+        assert compared >= max(1, T - 1)
+    rl.close()

@@ -110,3 +110,60 @@ def test_moe_stack_is_residual_chain(orc):
     for L in layers:
         y = (orc.moe_ffn(L, y, 1)[0] + y).astype(np.float32)
     assert np.array_equal(got, y)
+
+
+def _f64_layer_f32(hl, x, sel, w, gate_on_q8k=False, swap_gate_up=False):
+    """The QMA_NOQ8K layer (nn.c:393-407, 475-492, 576-629) in fp64 from the
+    closed-form dequantised weights; the two flags plant plausible mistakes
+    (the q8k path's shared gate on Q8_K(x); silu taken of the up dot)."""
+    N, F, E = hl.n_embd, hl.n_ff, hl.n_expert
+    x64 = x.astype(np.float64)
+
+    def deq(raw, wtype, rows, cols):
+        f = onp.q4k_dequant if wtype == 12 else onp.q6k_dequant
+        return f(raw).astype(np.float64).reshape(rows, cols)
+
+    def expert(ge, ue, de, dt):
+        g = deq(ge, 12, F, N) @ x64
+        u = deq(ue, 12, F, N) @ x64
+        if swap_gate_up:
+            g, u = u, g
+        h = g / (1.0 + np.exp(-g)) * u
+        return deq(de, dt, N, F) @ h
+
+    gb, db = hl.gate_exps.size // E, hl.down_exps.size // E
+    out = np.zeros(N)
+    for k, e in enumerate(sel):
+        out += np.float64(w[k]) * expert(hl.gate_exps[e * gb:(e + 1) * gb], hl.up_exps[e * gb:(e + 1) * gb],
+                                         hl.down_exps[e * db:(e + 1) * db], hl.t_down_exps)
+    if gate_on_q8k:
+        xq, xd, _ = onp.q8k_quant(x)
+        xin = xq.astype(np.float64) * np.repeat(xd.astype(np.float64), 256)
+    else:
+        xin = x64
+    gs = 1.0 / (1.0 + np.exp(-(hl.gate_inp_shexp.astype(np.float64) @ xin)))
+    return out + gs * expert(hl.gate_shexp, hl.up_shexp, hl.down_shexp, hl.t_down_shexp)
+
+
+@pytest.mark.parametrize("t_down", [14, 12])
+def test_moe_ffn_f32_vs_fp64(orc, t_down):
+    """orc_moe_ffn_f32 (the fp32 twin) against its fp64 closed form on the
+    oracle's own routing, within 2e-5 of max|out| (fp32 dots of 512 and 256
+    terms); the shared gate on Q8_K(x) and silu of the wrong dot each move the
+    output well beyond that bound, so the check tells them apart.  Also the
+    known distance to the q8k layer (activation quantisation, ~1e-2 here)."""
+    hl = make_host_layer(orc, seed=21, n_embd=512, n_ff=256, n_expert=16, n_used=4, t_down=t_down)
+    x = orc.fill_normal(8, 2 * 512, 0.0, 1.0)
+    got = orc.moe_ffn_f32(hl, x, 2)
+    for t in range(2):
+        xt = x[t * 512:(t + 1) * 512]
+        sel, w, _ = orc.moe_route(hl, xt)
+        ref = _f64_layer_f32(hl, xt, sel, w)
+        scale = np.max(np.abs(ref))
+        err = np.max(np.abs(got[t] - ref)) / scale
+        assert err < 2e-5, err
+        for wrong in (dict(gate_on_q8k=True), dict(swap_gate_up=True)):
+            alt = _f64_layer_f32(hl, xt, sel, w, **wrong)
+            assert np.max(np.abs(alt - ref)) / scale > 10 * 2e-5, wrong
+        q8 = orc.moe_ffn(hl, xt, 1)[0]
+        assert 1e-4 < np.max(np.abs(q8 - got[t])) / scale < 5e-2
