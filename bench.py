@@ -18,6 +18,7 @@ projection shapes at T = 1, and device sampling over the vocabulary.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -42,12 +43,29 @@ TOKEN_BYTES = N_LAYER * LAYER_TOKEN_BYTES                      # 818,544,640
 GATEUP_LAUNCH_BYTES = (N_USED + 1) * 2 * N_FF * Q4K_ROW + N_EMBD + 32 + 256 + (N_USED + 1) * N_FF * 4
 DOWN_LAUNCH_BYTES = (N_USED + 1) * N_EMBD * Q6K_ROW + (N_USED + 1) * (N_FF + 8 + 64) + 4 * N_EMBD * 2
 METRIC = "MoE FFN decode tokens/s + achieved HBM GB/s (% of peak), Q4_K/Q6_K, 1 GPU"
-# HBM bytes per launch of the fused decode kernel as built from this tree,
-# from two rocprofv3 counter passes over bench.py (FETCH_SIZE x 2.000 +
-# WRITE_SIZE x 1.000, the factors read off a 1 GiB copy kernel in the same
-# runs, profiles/moe_decode_kernel_c4_hbm_counters.md); re-measured whenever
-# the kernel changes.
-FUSED_TRAFFIC_BYTES = 869.8e6
+# HBM bytes per launch of the fused decode kernel, from two rocprofv3 counter
+# passes over bench.py (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors
+# read off a 1 GiB copy kernel in the same runs), with the profile holding
+# them and the SHA-256 (first 16 hex digits) of the kernel source they were
+# taken on.  The figure is reported only while that source is unchanged: an
+# edit to the kernel needs new counter passes (and a new entry here).
+FUSED_TRAFFIC = {"bytes": 869.0e6, "profile": "profiles/moe_decode_kernel_c4_hbm_counters.md",
+                 "source": "qwen-mobile-agent_amd/csrc/qmag_fused.hip", "source_sha16": "991d0b51549ad807"}
+
+
+def fused_traffic() -> tuple:
+    """(HBM bytes per decode launch or None, where the figure comes from)."""
+    try:
+        with open(os.path.join(ROOT, FUSED_TRAFFIC["source"]), "rb") as f:
+            sha = hashlib.sha256(f.read()).hexdigest()[:16]
+    except OSError:
+        sha = None
+    same = sha == FUSED_TRAFFIC["source_sha16"]
+    info = {"profile": FUSED_TRAFFIC["profile"], "measured_on_source_sha16": FUSED_TRAFFIC["source_sha16"],
+            "current_source_sha16": sha}
+    if not same:
+        info["note"] = "kernel source changed since the counter passes: traffic not reported"
+    return (FUSED_TRAFFIC["bytes"] if same else None), info
 
 
 def log(msg: str) -> None:
@@ -533,10 +551,12 @@ def main() -> int:
         avg_us = t_d / n_d * 1e3
     roofline = {"bound": "hbm", "kernel": kname,
                 "achieved": bytes_launch / (avg_us * 1e-6) / 1e9, "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s", "traffic": FUSED_TRAFFIC_BYTES if dom == "fused" else None,
+                "unit": "GB/s", "traffic": fused_traffic()[0] if dom == "fused" else None,
                 "bytes_per_launch": bytes_launch,
                 "avg_launch_us": avg_us, "avg_launch_us_event_pairs": t_d / n_d * 1e3}
     roofline["frac"] = roofline["achieved"] / roofline["peak"]
+    if dom == "fused":
+        roofline["traffic_source"] = fused_traffic()[1]
 
     if args.probe_copy_mb > 0:
         nb = args.probe_copy_mb << 20
