@@ -358,6 +358,15 @@ __device__ __forceinline__ float readlane_f(float v, int i)
 // sampler_pick (sampler.c:100-134) with candidate i in lane i (i < k, in
 // descending order); every lane returns the token.  *drew = 1 when a draw
 // was made (the seed advanced; the token joins last_tokens).
+//
+// The reference's three running sums, without a branch per candidate: a
+// lane that is not live contributes +0.0, which leaves a sum >= 0 unchanged,
+// so z adds every lane's value in index order, and lane i forms its own
+// inclusive prefix of p in index order -- the value the reference's acc and
+// cum (the same additions in the same order) hold after candidate i.  The
+// top-p cut is then the first live lane whose prefix reaches top_p (else the
+// last live lane), and the pick the first kept live lane whose prefix
+// exceeds the draw (else the last kept one): one ballot each.
 __device__ int samp_pick_wave(float lg, int id, int k, float temp, float top_p, uint64_t &seed, int *drew)
 {
     const int lane = lane_id();
@@ -374,32 +383,53 @@ __device__ int samp_pick_wave(float lg, int id, int k, float temp, float top_p, 
     // expf correctly rounded, through double (the device's expf is not)
     const float e = live ? (float)exp((double)__fsub_rn(lg, mx)) : 0.0f;
     double z = 0.0;                                        // summed in index order
-    for (int i = first_live; i < k; i++)
-        if ((lv >> i) & 1ull) z += (double)readlane_f(e, i);
+    for (int i = first_live; i < k; i++) z += (double)readlane_f(e, i);
     const float inv = (float)(1.0 / z);
-    const float p = __fmul_rn(e, inv);
-    float acc = 0.0f;
-    int kept = first_live;
-    for (int i = first_live; i < k; i++) {
-        if (!((lv >> i) & 1ull)) continue;
-        acc = __fadd_rn(acc, readlane_f(p, i));
-        kept = i + 1;
-        if (acc >= top_p) break;
+    const float p = live ? __fmul_rn(e, inv) : 0.0f;
+    float pre = 0.0f;                                      // p[first_live] + ... + p[lane], in order
+    for (int j = first_live; j < k; j++) {
+        const float s = __fadd_rn(pre, readlane_f(p, j));
+        pre = j <= lane ? s : pre;
     }
+    const unsigned long long hit = __ballot(live && pre >= top_p);
+    const int kept = hit ? __ffsll(hit) : 64 - __clzll(lv);        // the cut lane + 1
     const uint64_t r = samp_rng(seed);
     const float rv = (float)((double)(r >> 11) * (1.0 / 9007199254740992.0));
-    float cum = 0.0f;
-    int pick = kept - 1;
-    for (int i = first_live; i < kept; i++) {
-        if (!((lv >> i) & 1ull)) continue;
-        cum = __fadd_rn(cum, readlane_f(p, i));
-        if (rv < cum) {
-            pick = i;
-            break;
-        }
-    }
+    const unsigned long long pk = __ballot(live && lane < kept && rv < pre);
+    const int pick = pk ? __ffsll(pk) - 1 : kept - 1;
     *drew = 1;
     return __builtin_amdgcn_readlane(id, pick);
+}
+
+// The k largest of the chunks' candidates (total_c of them, E per thread),
+// sorted descending into s_win, or (return false) selected into s_win in no
+// order by the radix select.
+template <int E>
+__device__ bool samp_merge(const uint64_t *cand, int total_c, int k, uint64_t *s_win, uint64_t *s_sort, int *s_w,
+                           uint64_t *s_m, uint32_t *s_hist, int *s_info)
+{
+    const int t = (int)threadIdx.x;
+    uint64_t g[E];
+#pragma unroll
+    for (int j = 0; j < E; j++) {
+        const int i = t + 256 * j;
+        g[j] = i < total_c ? __hip_atomic_load(cand + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+    }
+    const bool sorted = wg_topk_sorted<E>(g, k, s_win, s_sort, s_w, s_m);
+    if (!sorted) {
+        bool gs[E];
+        wg_topk<E>(g, k, gs, s_hist, s_info, s_m);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < E; j++) cnt += gs[j];
+        int total;
+        int pos = wg_excl_scan(cnt, s_w, &total);
+#pragma unroll
+        for (int j = 0; j < E; j++)
+            if (gs[j]) s_win[pos++] = g[j];
+        __syncthreads();
+    }
+    return sorted;
 }
 
 // out (pinned host memory): [0..63] ids, [64..127] values (float bits),
@@ -420,37 +450,61 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
     float *s_v = (float *)s_v4;
     const int t = (int)threadIdx.x;
     const int base = (int)blockIdx.x * SAMP_CHUNK;
+    // the repeat penalty's ids and counts (argument memory) requested ahead
+    // of the logits, so that their round trip overlaps the logits' own
+    int pen_id = -1, pen_cnt = 0;
+    if (P.repeat_penalty != 1.0f && t < P.n_uniq) {
+        pen_id = P.uniq[t];
+        pen_cnt = P.count[t];
+    }
+    // the temperature in a register now, not reloaded after the barriers
+    uint32_t temp_bits = __float_as_uint(P.temp);
+    __asm__ volatile("" : "+s"(temp_bits));
+    const float temp = __uint_as_float(temp_bits);
+    if (base + SAMP_CHUNK <= n) {
+        // a whole chunk: every load in flight at once
+        float4 v[SAMP_PER_THREAD / 4];
 #pragma unroll
-    for (int m = 0; m < SAMP_PER_THREAD / 4; m++) {
-        const int i = base + 4 * (t + 256 * m);
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i + 3 < n) v = ldg4(logits + i);
-        else {
-            if (i < n) v.x = logits[i];
-            if (i + 1 < n) v.y = logits[i + 1];
-            if (i + 2 < n) v.z = logits[i + 2];
+        for (int m = 0; m < SAMP_PER_THREAD / 4; m++) v[m] = ldg4(logits + base + 4 * (t + 256 * m));
+#pragma unroll
+        for (int m = 0; m < SAMP_PER_THREAD / 4; m++) s_v4[t + 256 * m] = v[m];
+    } else {
+#pragma unroll
+        for (int m = 0; m < SAMP_PER_THREAD / 4; m++) {
+            const int i = base + 4 * (t + 256 * m);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i + 3 < n) v = ldg4(logits + i);
+            else {
+                if (i < n) v.x = logits[i];
+                if (i + 1 < n) v.y = logits[i + 1];
+                if (i + 2 < n) v.z = logits[i + 2];
+            }
+            s_v4[t + 256 * m] = v;
         }
-        s_v4[t + 256 * m] = v;
     }
     __syncthreads();
     // repeat penalty (sampler.c:47-55): each occurrence of an id in
     // last_tokens applies the rule to the current value, in turn
-    if (P.repeat_penalty != 1.0f && t < P.n_uniq) {
-        const int id = P.uniq[t];
-        if (id >= base && id < base + SAMP_CHUNK && id < n) {
-            float v = s_v[id - base];
-            for (int j = 0; j < P.count[t]; j++) v = v < 0.0f ? v * P.repeat_penalty : v / P.repeat_penalty;
-            s_v[id - base] = v;
-        }
+    if (pen_id >= base && pen_id < base + SAMP_CHUNK && pen_id < n) {
+        float v = s_v[pen_id - base];
+        for (int j = 0; j < pen_cnt; j++) v = v < 0.0f ? v * P.repeat_penalty : v / P.repeat_penalty;
+        s_v[pen_id - base] = v;
     }
     __syncthreads();
+    // element i = t + 256 m of the chunk: every LDS read issued at once
+    // (the chunk's slots past n hold zeros and are masked after)
+    float cv[SAMP_PER_THREAD];
+#pragma unroll
+    for (int m = 0; m < SAMP_PER_THREAD; m++) cv[m] = s_v[t + 256 * m];
+    if (temp > 0.0f && temp != 1.0f) {                            // sampler.c:56-58 (x / 1 = x)
+#pragma unroll
+        for (int m = 0; m < SAMP_PER_THREAD; m++) cv[m] = cv[m] / temp;
+    }
     uint64_t c[SAMP_PER_THREAD];
 #pragma unroll
     for (int m = 0; m < SAMP_PER_THREAD; m++) {
-        const int i = t + 256 * m;               // element i of the chunk
-        float v = s_v[i];
-        if (P.temp > 0.0f && P.temp != 1.0f) v = v / P.temp;     // sampler.c:56-58 (x / 1 = x)
-        c[m] = base + i < n ? samp_comp(samp_key(v), base + i) : 0ull;
+        const int i = t + 256 * m;
+        c[m] = base + i < n ? samp_comp(samp_key(cv[m]), base + i) : 0ull;
     }
     const int valid = n - base < SAMP_CHUNK ? n - base : SAMP_CHUNK;
     const int kk = k < valid ? k : valid;
@@ -484,28 +538,14 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
                  (unsigned)(n_chunks - 1);
     __syncthreads();
     if (!s_last) return;
-    uint64_t g[SAMP_MERGE_PER_THREAD];
+    // the k largest of all chunks' candidates: 8 per thread when they fit
+    // (up to 2,048: 38 chunks of 40 for a 151,936-entry vocabulary), the
+    // full 32 otherwise
     const int total_c = n_chunks * k;
-#pragma unroll
-    for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++) {
-        const int i = t + 256 * j;
-        g[j] = i < total_c ? __hip_atomic_load(cand + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-    }
-    // the k largest of all chunks' candidates, sorted descending into s_win
-    const bool sorted = wg_topk_sorted<SAMP_MERGE_PER_THREAD>(g, k, s_win, s_sort, s_w, s_m);
-    if (!sorted) {
-        bool gs[SAMP_MERGE_PER_THREAD];
-        wg_topk<SAMP_MERGE_PER_THREAD>(g, k, gs, s_hist, s_info, s_m);
-        int cnt = 0;
-#pragma unroll
-        for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++) cnt += gs[j];
-        int total;
-        int pos = wg_excl_scan(cnt, s_w, &total);
-#pragma unroll
-        for (int j = 0; j < SAMP_MERGE_PER_THREAD; j++)
-            if (gs[j]) s_win[pos++] = g[j];
-        __syncthreads();
-    }
+    const bool sorted = total_c <= 256 * 8
+                            ? samp_merge<8>(cand, total_c, k, s_win, s_sort, s_w, s_m, s_hist, s_info)
+                            : samp_merge<SAMP_MERGE_PER_THREAD>(cand, total_c, k, s_win, s_sort, s_w, s_m, s_hist,
+                                                                s_info);
     if (t < 64) {
         const int lane = t;
         uint64_t v = lane < k ? s_win[lane] : 0ull;
@@ -522,7 +562,7 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
         if (sample) {
             int drew = 0;
             uint64_t sd = seed;
-            const int tok = samp_pick_wave(val, id, k, P.temp, top_p, sd, &drew);
+            const int tok = samp_pick_wave(val, id, k, temp, top_p, sd, &drew);
             if (lane == 0) {
                 put(128, tok);
                 put(129, drew);
