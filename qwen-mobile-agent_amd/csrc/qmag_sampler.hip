@@ -288,53 +288,107 @@ __device__ __forceinline__ void wave_sort128(uint64_t &a, uint64_t &b)
         }
 }
 
+// 32-bit forms of the networks above, for keys without the index half
+__device__ __forceinline__ uint32_t bitonic_step32(uint32_t v, int i, int size, int stride)
+{
+    const uint32_t o = xor_lane(v, stride);
+    const bool keep_max = ((i & stride) == 0) == ((i & size) == 0);
+    return (v > o) == keep_max ? v : o;
+}
+__device__ __forceinline__ uint32_t wave_sort64_u32(uint32_t v)
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) v = bitonic_step32(v, lane, size, stride);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_clean64_u32(uint32_t v)
+{
+    const int lane = lane_id();
+    v = bitonic_step32(v, lane, 64, 32);
+    v = bitonic_step32(v, lane, 64, 16);
+    v = bitonic_step32(v, lane, 64, 8);
+    v = bitonic_step32(v, lane, 64, 4);
+    v = bitonic_step32(v, lane, 64, 2);
+    return bitonic_step32(v, lane, 64, 1);
+}
+// 32 keys in lanes 0-31 sorted descending (lanes 32-63 sort their own 32)
+__device__ __forceinline__ uint64_t wave_sort32(uint64_t v)
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= 32; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) v = bitonic_step(v, lane, size, stride);
+    return v;
+}
+
 // The `need` (<= 64) largest nonzero keys held across the workgroup (E per
 // thread, all distinct), sorted descending into s_out[0..need), by sorting
-// networks instead of radix passes: the need-th largest of the threads'
+// networks instead of radix passes.  The need-th largest of the threads'
 // maxima bounds the answer from below (need threads hold a key at least
-// that large; it comes from the four waves' sorted maxima merged twice), and
-// when at most 128 keys reach the bound one wave sorts them.  Returns false
-// (nothing written, c untouched) when more reach it; the caller then takes
-// the radix select.  s_sort: 256 uint64, s_w: 4 ints, s_m: 4 uint64.
+// that large); only its value half is found (32-bit networks: the four
+// waves' sorted maxima merged twice), and every key whose value half reaches
+// it is kept -- a superset of the keys at or above the full bound, so it
+// holds the answer.  The kept keys are gathered through an LDS counter (in
+// no fixed order) and, when at most 128, sorted by one wave: the sorted
+// result is the same whatever order they were gathered in.  Returns false
+// (nothing written to s_out, c untouched) when more than 128 are kept; the
+// caller then takes the radix select.  s_sort: 256 uint64, s_w: 4 ints.
 template <int E>
 __device__ bool wg_topk_sorted(const uint64_t (&c)[E], int need, uint64_t *s_out, uint64_t *s_sort, int *s_w,
                                uint64_t *s_m)
 {
+    (void)s_m;
     const int t = (int)threadIdx.x, w = t >> 6, lane = t & 63;
     uint64_t m = 0;
 #pragma unroll
     for (int j = 0; j < E; j++) m = c[j] > m ? c[j] : m;
-    s_sort[t] = wave_sort64(m);
+    uint32_t *s_s32 = (uint32_t *)s_sort;
+    if (t == 0) s_w[0] = 0;                   // the kept-key counter, used after three barriers
+    s_s32[t] = wave_sort64_u32((uint32_t)(m >> 32));
     __syncthreads();
-    uint64_t v2 = 0;
+    uint32_t v2 = 0;
     if (w < 2) {                              // top 64 of waves (0, 1) and of (2, 3)
-        const uint64_t x = s_sort[128 * w + lane], y = s_sort[128 * w + 127 - lane];
-        v2 = wave_clean64(x > y ? x : y);
+        const uint32_t x = s_s32[128 * w + lane], y = s_s32[128 * w + 127 - lane];
+        v2 = wave_clean64_u32(x > y ? x : y);
     }
     __syncthreads();                          // every read above is done
-    if (w < 2) s_sort[64 * w + lane] = v2;
+    if (w < 2) s_s32[64 * w + lane] = v2;
     __syncthreads();
     if (w == 0) {                             // top 64 of all the maxima
-        const uint64_t x = s_sort[lane], y = s_sort[127 - lane];
-        const uint64_t v = wave_clean64(x > y ? x : y);
-        const uint64_t bound = readlane64(v, need - 1);
-        if (lane == 0) s_m[0] = bound;
+        const uint32_t x = s_s32[lane], y = s_s32[127 - lane];
+        const uint32_t v = wave_clean64_u32(x > y ? x : y);
+        const uint32_t bound = (uint32_t)__builtin_amdgcn_readlane((int)v, need - 1);
+        if (lane == 0) s_w[1] = (int)bound;
     }
     __syncthreads();
-    const uint64_t bound = s_m[0];            // 0 when fewer than `need` threads hold keys
+    const uint32_t bound = (uint32_t)s_w[1];  // 0 when fewer than `need` threads hold keys
     int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < E; j++) cnt += c[j] && c[j] >= bound;
-    int total;
-    int pos = wg_excl_scan(cnt, s_w, &total);
-    if (total > 128) return false;            // workgroup-uniform
+    for (int j = 0; j < E; j++) cnt += c[j] && (uint32_t)(c[j] >> 32) >= bound;
+    int pos = cnt ? atomicAdd(&s_w[0], cnt) : 0;
 #pragma unroll
     for (int j = 0; j < E; j++)
-        if (c[j] && c[j] >= bound) s_sort[pos++] = c[j];
+        if (c[j] && (uint32_t)(c[j] >> 32) >= bound) {
+            if (pos < 128) s_sort[pos] = c[j];
+            pos++;
+        }
     __syncthreads();
+    const int total = s_w[0];
+    if (total > 128) return false;            // workgroup-uniform
     if (w == 0) {
-        uint64_t a = lane < total ? s_sort[lane] : 0ull, b = 64 + lane < total ? s_sort[64 + lane] : 0ull;
-        wave_sort128(a, b);
+        uint64_t a = lane < total ? s_sort[lane] : 0ull;
+        if (total <= 32) {                    // the usual case
+            a = wave_sort32(a);
+        } else if (total <= 64) {
+            a = wave_sort64(a);
+        } else {
+            uint64_t b = 64 + lane < total ? s_sort[64 + lane] : 0ull;
+            wave_sort128(a, b);
+        }
         if (lane < need) s_out[lane] = a;
     }
     __syncthreads();
