@@ -10,15 +10,15 @@
 // One launch of one workgroup per 4096 logits.  Each workgroup applies the
 // penalty and the temperature to its logits and selects its k largest over
 // unique 64-bit keys (the value's order-preserving bits, then the
-// complemented index, so equal values order by ascending index): the k-th
-// largest of the threads' maxima bounds the answer from below, and the few
-// keys that reach it are sorted by one wave's bitonic network (an exact
-// radix select takes over when more than 128 reach it).  The last workgroup
-// to finish (a device-scope counter) selects the k largest of all chunks'
-// candidates the same way and, in the sampling form, makes the pick with the
-// reference's arithmetic, the candidates one per lane and the sequential
-// sums as uniform loops over the lanes.  Results are written straight to
-// pinned host memory.
+// complemented index, so equal values order by ascending index): the value
+// half of the k-th largest of the threads' maxima bounds the answer from
+// below, and the few keys that reach it are sorted by one wave's bitonic
+// network (an exact radix select takes over when more than 128 reach it).
+// The last workgroup to finish (a device-scope counter) selects the k
+// largest of all chunks' candidates the same way and, in the sampling form,
+// makes the pick with the reference's arithmetic, the candidates one per
+// lane: the sequential sums become per-lane prefixes in the same order, and
+// each cut one ballot.  Results are written straight to pinned host memory.
 //
 // Among exactly equal values the lower index comes first.  The reference
 // keeps its candidates in a min-heap and sorts them with qsort, so which of
