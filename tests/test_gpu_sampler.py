@@ -152,6 +152,36 @@ def test_sample_all_masked(qm, orc):
     assert sd.seed == 9 and sd.n_last == 0
 
 
+@pytest.mark.parametrize("case", ["partly_masked", "one_inf", "masked_and_inf"])
+def test_sample_edge_candidates_vs_oracle(qm, orc, case):
+    """Candidate lists the pick's per-lane sums must treat as the reference's
+    running sums do: fewer live logits than top_k (the masked ones, -1e30,
+    fill the list's tail and are skipped), and a +Inf logit (its softmax term
+    is NaN, so every probability is NaN: no cut, the pick falls to the last
+    live candidate).  Tokens, seeds and histories equal the oracle's over a
+    short sequence."""
+    rng = np.random.default_rng({"partly_masked": 5, "one_inf": 6, "masked_and_inf": 7}[case])
+    kw = dict(seed=777, temp=0.9, top_k=20, top_p=0.9, repeat_penalty=1.0)
+    sd, so = _state(qm, orc, **kw)
+    d = qm.DBuf(4 * V)
+    for step in range(12):
+        logits = (rng.standard_normal(V) * 2.0).astype(np.float32)
+        if case != "one_inf":
+            live = rng.choice(V, 11, replace=False)
+            masked = np.full(V, -1e30, np.float32)
+            masked[live] = logits[live]
+            logits = masked
+        if case != "partly_masked":
+            logits[rng.integers(V)] = np.inf
+        d.upload(logits)
+        gt = qm.sampler_sample_dev(d.ptr, V, sd, 40, 0.9)
+        oi, ov = orc.sampler_candidates(logits, so, 40)
+        ot = orc.sampler_pick(so, oi, ov, 0.9)
+        assert gt == ot, step
+        assert sd.seed == so.seed and sd.n_last == so.n_last, step
+        assert list(sd.last_tokens)[:sd.n_last] == list(so.last_tokens)[:so.n_last], step
+
+
 def test_sample_after_recovery_reports_stale_logits(qm, orc):
     """A persistent decode launch queued before the sampler finds its abort
     word set (the test hook, as after an expired wait).  The sampler's status
