@@ -165,17 +165,16 @@ def aux_matvec(name: str, n_in: int, n_out: int, wtype: int, copies: int, second
     baseline is the oracle's matmul (mm_worker rows over min(nproc, 16)
     pool threads, nn.c:276-303) on the first copy's bytes.  With `repack`
     the Q6_K matrices are repacked once (qmag_repack_q6k_dev, outside the
-    timed region) and timed as QMAG_TYPE_Q6_K_R: the same bytes and results."""
+    timed region, in place) and timed as QMAG_TYPE_Q6_K_R: the same bytes and
+    results."""
     rb = n_in // 256 * (144 if wtype == 12 else 210)
     Ws = [qmag.DBuf(rb * n_out) for _ in range(copies)]
     for i, w in enumerate(Ws):
         qmag.synth_weights(0xC100 + i, n_in * n_out, 0.02, wtype, w.ptr)
     if repack:
-        Rs = [qmag.DBuf(rb * n_out) for _ in range(copies)]
-        for w, r in zip(Ws, Rs):
-            qmag.repack_q6k_dev(w, r, n_in, n_out)
-            w.close()
-        Ws, wtype = Rs, qmag.TYPE_Q6_K_R
+        for w in Ws:
+            qmag.repack_q6k_dev(w, w, n_in, n_out)          # in place
+        wtype = qmag.TYPE_Q6_K_R
     x = qmag.DBuf(4 * n_in)
     qmag.synth_normal(0xC1, n_in, 0.0, 1.0, x.ptr)
     out = qmag.DBuf(4 * n_out)

@@ -211,8 +211,10 @@ int qmag_matmul_group_dev(const float *x, int n_in, int n_mat, const void *const
    bytes, the scales and the d values of every super-block (n_out * n_in / 256
    * 210 bytes, as before).  No counterpart in the reference: a one-time
    transform at weight upload for large Q6_K matrices such as the LM head
-   (nn.c:2243).  dst: device memory of the same size, 16-byte aligned, not
-   overlapping src.  Results of qmag_matmul_dev / qmag_matmul_q8k_dev /
+   (nn.c:2243).  dst: device memory of the same size, 16-byte aligned, either
+   src itself (the rows are repacked in place, each through LDS, so no second
+   copy of the matrix is needed; rows of at most 65,536 bytes, n_in <= 79,872)
+   or not overlapping it.  Results of qmag_matmul_dev / qmag_matmul_q8k_dev /
    qmag_matmul_noalloc_dev on the repacked rows are bit-identical to those on
    the block layout. */
 int qmag_repack_q6k_dev(const void *src, void *dst, int n_in, int n_out);

@@ -164,6 +164,33 @@ __global__ __launch_bounds__(256) void repack_q6k_kernel(const uint8_t *__restri
     rp[208 * nb + 2 * ib + 1] = b[209];
 }
 
+// The same transform in place: one workgroup per row reads the whole row
+// into LDS before any byte of it is written back (rows are independent), so
+// no second copy of the matrix is needed.  Destination byte o of the row
+// takes the block-layout byte the out-of-place kernel puts there.
+__device__ __forceinline__ int repack_src(int o, int nb)
+{
+    if (o < 128 * nb) {                           // the low, then the high ql planes
+        const int hi = o >= 64 * nb, r = hi ? o - 64 * nb : o;
+        const int ib = r / 64, q = (r % 64) / 16, j = r % 16;
+        return ib * Q6K_BYTES + 64 * (q >> 1) + 32 * hi + 16 * (q & 1) + j;
+    }
+    if (o < 192 * nb) return ((o - 128 * nb) / 64) * Q6K_BYTES + 128 + (o - 128 * nb) % 64;   // qh
+    if (o < 208 * nb) return ((o - 192 * nb) / 16) * Q6K_BYTES + 192 + (o - 192 * nb) % 16;   // scales
+    return ((o - 208 * nb) / 2) * Q6K_BYTES + 208 + (o - 208 * nb) % 2;                       // d
+}
+__global__ __launch_bounds__(256) void repack_q6k_inplace_kernel(uint8_t *__restrict__ W, int nb)
+{
+    extern __shared__ uint8_t s_row[];
+    const int rb = nb * Q6K_BYTES;
+    uint8_t *rp = W + (size_t)blockIdx.x * rb;
+    for (int i = (int)threadIdx.x; i < rb; i += 256) s_row[i] = rp[i];
+    __syncthreads();
+    for (int o = (int)threadIdx.x; o < rb; o += 256) rp[o] = s_row[repack_src(o, nb)];
+}
+
+constexpr int REPACK_INPLACE_MAX_ROW = 65536;     // bytes of a row staged in LDS
+
 int launch_repack_q6k(const void *src, void *dst, int n_in, int n_out, hipStream_t s)
 {
     if (n_in <= 0 || n_in % (8 * QK_K) || n_out <= 0)
@@ -172,7 +199,18 @@ int launch_repack_q6k(const void *src, void *dst, int n_in, int n_out, hipStream
         return fail(QMAG_ERR_ARG, "repack_q6k: null or unaligned pointer (dst needs 16-byte alignment)");
     const size_t bytes = (size_t)n_out * (n_in / QK_K) * Q6K_BYTES;
     const uintptr_t a = (uintptr_t)src, b = (uintptr_t)dst;
-    if (a < b + bytes && b < a + bytes) return fail(QMAG_ERR_ARG, "repack_q6k: src and dst overlap");
+    if (a == b) {
+        const int nb = n_in / QK_K, rb = nb * Q6K_BYTES;
+        if (rb > REPACK_INPLACE_MAX_ROW)
+            return fail(QMAG_ERR_ARG, "repack_q6k: in place needs rows of at most %d bytes (n_in=%d)",
+                        REPACK_INPLACE_MAX_ROW, n_in);
+        hipLaunchKernelGGL(repack_q6k_inplace_kernel, dim3((unsigned)n_out), dim3(256), (size_t)rb, s,
+                           (uint8_t *)dst, nb);
+        QMAG_HIP(hipGetLastError());
+        return QMAG_OK;
+    }
+    if (a < b + bytes && b < a + bytes)
+        return fail(QMAG_ERR_ARG, "repack_q6k: src and dst overlap without being the same buffer");
     const long nblocks = (long)n_out * (n_in / QK_K);
     hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, s,
                        (const uint8_t *)src, (uint8_t *)dst, n_in / QK_K, nblocks);

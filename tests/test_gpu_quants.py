@@ -263,6 +263,9 @@ def test_q6k_repacked_rows_match_block_layout(qm, orc, n_in, n_out):
     Rb = qm.DBuf(W.nbytes)
     qm.repack_q6k_dev(Wb, Rb, n_in, n_out)
     assert np.array_equal(Rb.download(np.uint8), _repack_layout(W, n_in, n_out))
+    Ib = qm.DBuf.from_array(W)
+    qm.repack_q6k_dev(Ib, Ib, n_in, n_out)                 # in place: the same bytes
+    assert np.array_equal(Ib.download(np.uint8), Rb.download(np.uint8))
     L = qm.lib()
     for T in (1, 3):
         x = orc.fill_normal(7100 + T, T * n_in, 0.0, 1.0)
@@ -285,14 +288,25 @@ def test_q6k_repacked_rows_match_block_layout(qm, orc, n_in, n_out):
     assert np.array_equal(a.download(np.uint32), b.download(np.uint32))
 
 
+def test_q6k_repack_in_place_longest_row(qm, orc):
+    """In place, the longest row the LDS staging takes (n_in 79,872: 65,520
+    bytes) and a few rows: the documented layout, byte for byte."""
+    n_in, n_out = 39 * 2048, 3
+    W = orc.quantize(orc.fill_normal(7300, n_in * n_out, 0.0, 0.02), 14)
+    Ib = qm.DBuf.from_array(W)
+    qm.repack_q6k_dev(Ib, Ib, n_in, n_out)
+    assert np.array_equal(Ib.download(np.uint8), _repack_layout(W, n_in, n_out))
+
+
 def test_q6k_repacked_lm_head_shape(qm, orc):
-    """The C2 shape (151,936 x 2048) repacked: bit-identical to the block
-    layout's output."""
+    """The C2 shape (151,936 x 2048) repacked in place (no second copy of the
+    255 MB matrix): bit-identical to the block layout's output."""
     n_in, n_out = 2048, 151936
     Wb = qm.DBuf(n_in // 256 * 210 * n_out)
     qm.synth_weights(42, n_in * n_out, 0.02, 14, Wb.ptr)
     Rb = qm.DBuf(Wb.nbytes)
-    qm.repack_q6k_dev(Wb, Rb, n_in, n_out)
+    qm.synth_weights(42, n_in * n_out, 0.02, 14, Rb.ptr)
+    qm.repack_q6k_dev(Rb, Rb, n_in, n_out)
     xb = qm.DBuf.from_array(orc.fill_normal(3, n_in, 0.0, 1.0))
     a, b = qm.DBuf(4 * n_out), qm.DBuf(4 * n_out)
     qm.matmul_dev(xb, Wb, n_in, n_out, 1, qm.TYPE_Q6_K, a)
@@ -301,15 +315,17 @@ def test_q6k_repacked_lm_head_shape(qm, orc):
 
 
 def test_q6k_repack_rejects_bad_arguments(qm):
-    """Row lengths that are not a multiple of 2048, unaligned or overlapping
-    buffers, and the repacked type at such lengths are argument errors."""
+    """Row lengths that are not a multiple of 2048, unaligned buffers, buffers
+    that overlap without being the same one, rows too long to repack in place,
+    and the repacked type at such lengths are argument errors."""
     L = qm.lib()
     W = qm.DBuf(8 * 210 * 64)
     R = qm.DBuf(8 * 210 * 64 + 64)
     x, out = qm.DBuf(4 * 2048), qm.DBuf(4 * 64)
     assert L.qmag_repack_q6k_dev(W.ptr, R.ptr, 1024, 64) == -2
     assert L.qmag_repack_q6k_dev(W.ptr, R.ptr + 8, 2048, 64) == -2
-    assert L.qmag_repack_q6k_dev(W.ptr, W.ptr, 2048, 64) == -2
+    assert L.qmag_repack_q6k_dev(W.ptr, W.ptr + 16, 2048, 63) == -2
+    assert L.qmag_repack_q6k_dev(W.ptr, W.ptr, 40 * 2048, 1) == -2
     assert L.qmag_matmul_dev(x.ptr, W.ptr, 1024, 64, 1, qm.TYPE_Q6_K_R, out.ptr) == -2
     assert L.qmag_matmul_dev(x.ptr, R.ptr + 8, 2048, 64, 1, qm.TYPE_Q6_K_R, out.ptr) == -2
     assert L.qmag_repack_q6k_dev(W.ptr, R.ptr, 2048, 64) == 0
