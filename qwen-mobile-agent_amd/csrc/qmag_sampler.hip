@@ -673,17 +673,26 @@ static int sample_run(int n_vocab, const float *logits, const qmag_sampler *s, i
     P.temp = s->temp;
     P.repeat_penalty = s->repeat_penalty;
     const int n_last = s->n_last < 0 ? 0 : s->n_last > 64 ? 64 : s->n_last;
+    // distinct ids in first-occurrence order with their counts, found through
+    // a 128-entry open-addressing table (at most 64 ids, so it never fills)
+    // instead of a linear search over the ids seen so far (up to ~2,000
+    // comparisons per call on the host, ahead of the launch)
+    short slot[128];                                    // index into P.uniq + 1, 0 = empty
+    int key[128];
+    memset(slot, 0, sizeof(slot));
     P.n_uniq = 0;
     for (int i = 0; i < n_last; i++) {
         const int id = s->last_tokens[i];
         if (id < 0 || id >= n_vocab) continue;             // sampler.c:50
-        int u = 0;
-        while (u < P.n_uniq && P.uniq[u] != id) u++;
-        if (u == P.n_uniq) {
+        unsigned h = ((unsigned)id * 2654435761u) >> 25;
+        while (slot[h] && key[h] != id) h = (h + 1) & 127;
+        if (!slot[h]) {
+            key[h] = id;
+            slot[h] = (short)(P.n_uniq + 1);
             P.uniq[P.n_uniq] = id;
             P.count[P.n_uniq++] = 0;
         }
-        P.count[u]++;
+        P.count[slot[h] - 1]++;
     }
     const int n_chunks = (n_vocab + SAMP_CHUNK - 1) / SAMP_CHUNK;
     hipStream_t st = ctx().stream;
