@@ -365,11 +365,26 @@ def aux_layer(cl, seconds: float, cpu_us_per_layer: float | None) -> dict:
            "bytes_per_call": LAYER_TOKEN_BYTES, "us_per_call": us,
            "gbps": LAYER_TOKEN_BYTES / (us * 1e-6) / 1e9}
     res["frac_of_peak"] = res["gbps"] * 1e9 / HBM_PEAK
+    # the same calls with x and out in host memory (qmag_moe_ffn_host, the
+    # engine's own moe_ffn call): the PCIe-inclusive rate, each call
+    # synchronous; wall time on the host, never the bench value
+    hx = np.zeros(N_EMBD, np.float32)
+    hx[:] = qmag.d2h_ptr(x.ptr, np.float32, N_EMBD)
+    for c in cl:
+        qmag.moe_ffn_host(c, hx, 1)
+    t0 = time.perf_counter()
+    n_host = 0
+    while time.perf_counter() - t0 < seconds / 4 or n_host < len(cl):
+        for c in cl:
+            qmag.moe_ffn_host(c, hx, 1)
+        n_host += len(cl)
+    res["host_buffers_us_per_call"] = (time.perf_counter() - t0) / n_host * 1e6
     if cpu_us_per_layer:
         res["cpu_baseline"] = {"us_per_call": cpu_us_per_layer, "kind": "port",
                                "cores": min(os.cpu_count() or 1, 8),
                                "sample": "per layer-token time of the C4 CPU sample"}
-    log(f"C3 layer: {us:.2f} us/call, {res['gbps']:.0f} GB/s")
+    log(f"C3 layer: {us:.2f} us/call, {res['gbps']:.0f} GB/s; "
+        f"with x and out in host memory {res['host_buffers_us_per_call']:.2f} us/call")
     return res
 
 

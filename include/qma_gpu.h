@@ -270,6 +270,16 @@ typedef struct qmag_moe_layer {
    sigmoid(gs) * shared(x[t]) for T tokens (x, out: f32 [T][n_embd]). */
 int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *out, int T);
 
+/* The moe_ffn seam on host buffers, as the engine calls it (nn.c:2246-2252:
+   moe_ffn(m, il, x, ..., out, T) with host pointers, out read at once): x and
+   out are host memory, f32 [T][n_embd].  x goes to the device through pinned
+   staging on the library stream, the layer runs as qmag_moe_ffn_dev, out
+   comes back the same way, and the call returns after one stream
+   synchronisation (the persistent decode kernel's status read in the same
+   pass; an expired wait is recovered before out is returned).  Synchronous;
+   one call at a time (an internal lock). */
+int qmag_moe_ffn_host(const qmag_moe_layer *L, const float *x, float *out, int T);
+
 /* The moe_ffn seam with q8k off (QMA_NOQ8K, or no q8k; nn.c:585): the same
    routing, then moe_expert_one and moe_shared (nn.c:393-407, 475-492) --
    expert h on fp32 x, the shared gate sigmoid(wsh . x) on fp32 x, every dot

@@ -1021,18 +1021,9 @@ static int replay(const std::vector<FusedCall> &log, const std::vector<qmag_moe_
     return QMAG_OK;
 }
 
-int fused_status()
+// the status once the abort word has been read (the stream synchronised)
+static int status_of_word(int word)
 {
-    g_pending = false;
-    if (!g_abort) {
-        g_log.clear();
-        g_log_layers.clear();
-        g_snap_used = 0;
-        return QMAG_OK;
-    }
-    QMAG_HIP(hipStreamSynchronize(ctx().stream));
-    int word = 0;
-    QMAG_HIP(hipMemcpy(&word, g_abort, sizeof(int), hipMemcpyDeviceToHost));
     g_snap_used = 0;
     if (word == 0) {                 // the common case: keep the storage's capacity
         g_log.clear();
@@ -1049,6 +1040,47 @@ int fused_status()
     if (st) return st;
     g_recovered++;
     return QMAG_OK;
+}
+
+int fused_status()
+{
+    g_pending = false;
+    if (!g_abort) {
+        g_log.clear();
+        g_log_layers.clear();
+        g_snap_used = 0;
+        return QMAG_OK;
+    }
+    QMAG_HIP(hipStreamSynchronize(ctx().stream));
+    int word = 0;
+    QMAG_HIP(hipMemcpy(&word, g_abort, sizeof(int), hipMemcpyDeviceToHost));
+    return status_of_word(word);
+}
+
+// For a caller that synchronises the stream anyway: the abort word is
+// copied into host memory (pinned) on the stream behind the launches, and
+// fused_status_word takes it after the synchronisation instead of reading
+// it with a second round trip.  No persistent launch yet: the word is 0.
+int fused_abort_copy(int *host, hipStream_t s)
+{
+    if (!g_abort) {
+        *host = 0;
+        return QMAG_OK;
+    }
+    QMAG_HIP(hipMemcpyAsync(host, g_abort, sizeof(int), hipMemcpyDeviceToHost, s));
+    return QMAG_OK;
+}
+
+int fused_status_word(int word)
+{
+    g_pending = false;
+    if (!g_abort) {
+        g_log.clear();
+        g_log_layers.clear();
+        g_snap_used = 0;
+        return QMAG_OK;
+    }
+    return status_of_word(word);
 }
 
 long fused_recoveries() { return g_recovered; }

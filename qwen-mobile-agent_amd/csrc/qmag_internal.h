@@ -49,6 +49,7 @@ enum WsSlot {
     WS_Y,                           // grouped prefill: per-pair down outputs
     WS_XMB,                         // grouped prefill: Q8_K(x) sub-block sums times the block scale
     WS_SAMP,                        // sampler: per-chunk candidates and the merged list
+    WS_HOSTIO,                      // qmag_moe_ffn_host: the device copies of x and out
     WS_COUNT
 };
 void *workspace(int slot, size_t bytes, int *status);
@@ -121,6 +122,8 @@ void fused_test_abort_next(int nth);
 // the launch sequence wrote the latest stage outputs (qmag_moe_last_stage)
 void moe_note_sequence_ran();
 int fused_status();
+int fused_abort_copy(int *host, hipStream_t s);
+int fused_status_word(int word);
 // true when a persistent decode launch was issued since the last status check
 bool fused_pending();
 int fused_trace_read(void *dst, size_t bytes);

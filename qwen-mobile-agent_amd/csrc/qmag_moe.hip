@@ -13,7 +13,9 @@
 //                   in the reference's combine order (k = 0..n_used-1, then shared),
 //                   optionally plus a residual                         nn.c:435-437, 468-472, 614-629
 #include <limits.h>
+#include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "qmag_internal.h"
@@ -688,6 +690,63 @@ extern "C" int qmag_moe_ffn_dev(const qmag_moe_layer *L, const float *x, float *
     }
     g_last_fused = false;
     return moe_ffn(L, x, out, T, nullptr, ctx().stream);
+}
+
+// The moe_ffn seam on host buffers: x staged through pinned memory and
+// copied to the device on the library stream, the layer queued behind it,
+// out copied back the same way together with the persistent decode kernel's
+// abort word, then one synchronisation.  Pinned staging is allocated (never
+// registered) and grown as needed; one call at a time.
+static std::mutex g_host_mu;
+static uint8_t *g_host_pin = nullptr;
+static size_t g_host_pin_cap = 0;
+
+extern "C" int qmag_moe_ffn_host(const qmag_moe_layer *L, const float *x, float *out, int T)
+{
+    int st = require_ready();
+    if (st) return st;
+    st = moe_check_layer(L);
+    if (st) return st;
+    if (!x || !out || T <= 0) return fail(QMAG_ERR_ARG, "moe_host: x=%p out=%p T=%d", x, out, T);
+    const size_t bytes = sizeof(float) * (size_t)T * L->n_embd, half = (bytes + 255) & ~(size_t)255;
+    std::lock_guard<std::mutex> guard(g_host_mu);
+    hipStream_t s = ctx().stream;
+    if (2 * half + 256 > g_host_pin_cap) {
+        if (g_host_pin) QMAG_HIP(hipHostFree(g_host_pin));   // no copy from it is pending: every call synchronises
+        g_host_pin = nullptr;
+        g_host_pin_cap = 0;
+        QMAG_HIP(hipHostMalloc((void **)&g_host_pin, 2 * half + 256, hipHostMallocDefault));
+        g_host_pin_cap = 2 * half + 256;
+    }
+    uint8_t *dev = (uint8_t *)workspace(WS_HOSTIO, 2 * half, &st);
+    if (!dev) return st;
+    float *pin_x = (float *)g_host_pin, *pin_out = (float *)(g_host_pin + half);
+    int *pin_word = (int *)(g_host_pin + 2 * half);
+    float *d_x = (float *)dev, *d_out = (float *)(dev + half);
+    memcpy(pin_x, x, bytes);
+    QMAG_HIP(hipMemcpyAsync(d_x, pin_x, bytes, hipMemcpyHostToDevice, s));
+    st = qmag_moe_ffn_dev(L, d_x, d_out, T);
+    if (st) return st;
+    QMAG_HIP(hipMemcpyAsync(pin_out, d_out, bytes, hipMemcpyDeviceToHost, s));
+    const bool pending = fused_pending();
+    if (pending) {
+        st = fused_abort_copy(pin_word, s);
+        if (st) return st;
+    }
+    QMAG_HIP(hipStreamSynchronize(s));
+    if (pending) {
+        // a persistent launch whose wait expired: the affected calls (this one
+        // among them) are re-run, then out is copied again
+        const long r0 = fused_recoveries();
+        st = fused_status_word(*pin_word);
+        if (st) return st;
+        if (fused_recoveries() != r0) {
+            QMAG_HIP(hipMemcpyAsync(pin_out, d_out, bytes, hipMemcpyDeviceToHost, s));
+            QMAG_HIP(hipStreamSynchronize(s));
+        }
+    }
+    memcpy(out, pin_out, bytes);
+    return QMAG_OK;
 }
 
 extern "C" int qmag_moe_stack_dev(const qmag_moe_layer *layers, int n_layer, float *x, int n_tok)

@@ -59,6 +59,7 @@ SIGNATURES = {
     "qmag_dequant_dev": (C.c_int, [P, C.c_int, C.c_int64, P]),
     "qmag_matmul_f32_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "qmag_moe_ffn_dev": (C.c_int, [P, P, P, C.c_int]),
+    "qmag_moe_ffn_host": (C.c_int, [P, P, P, C.c_int]),
     "qmag_moe_ffn_f32_dev": (C.c_int, [P, P, P, C.c_int]),
     "qmag_moe_stack_dev": (C.c_int, [P, C.c_int, P, C.c_int]),
     "qmag_moe_last_stage": (C.c_int, [C.POINTER(P)] * 5),
@@ -296,6 +297,14 @@ def matmul_f32_dev(x: DBuf, W: DBuf, n_in, n_out, T, wtype, out: DBuf) -> None:
 
 def moe_ffn_dev(layer: MoeLayer, x_ptr: int, out_ptr: int, T: int) -> None:
     check(lib().qmag_moe_ffn_dev(C.byref(layer), x_ptr, out_ptr, T))
+
+
+def moe_ffn_host(layer: MoeLayer, x: np.ndarray, T: int) -> np.ndarray:
+    """One MoE layer on host buffers (qmag_moe_ffn_host): x f32 [T * n_embd]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    check(lib().qmag_moe_ffn_host(C.byref(layer), x.ctypes.data_as(P), out.ctypes.data_as(P), T))
+    return out
 
 
 def moe_ffn_f32_dev(layer: MoeLayer, x_ptr: int, out_ptr: int, T: int) -> None:

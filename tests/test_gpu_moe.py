@@ -781,3 +781,43 @@ def test_moe_layer_f32_vs_oracle(qm, orc, cfg):
                 compared += 1
         assert compared >= max(1, T - 1)
     rl.close()
+
+
+@pytest.mark.parametrize("T", [1, 5, 16])
+def test_moe_ffn_host_equals_device(qm, orc, T):
+    """qmag_moe_ffn_host (x and out in host memory, the engine's moe_ffn call)
+    gives the bits of qmag_moe_ffn_dev on the same input: the persistent
+    one-layer kernel (T = 1), the launch sequence (T = 5) and the grouped
+    prefill (T = 16), the stage buffers those of the same path."""
+    rl = qm.ResidentLayer(seed=7, layer=1)
+    x = orc.fill_normal(90 + T, T * 2048, 0.0, 1.0)
+    want = run_layer(qm, rl, x, T).reshape(-1)
+    got = qm.moe_ffn_host(rl.c, x, T)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    again = qm.moe_ffn_host(rl.c, x, T)                # the staging reused
+    assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
+    rl.close()
+
+
+def test_moe_ffn_host_recovers_expired_wait(qm, orc):
+    """The host call's persistent launch finds its abort word set (the test
+    hook, as after an expired wait): the call itself re-runs the layer through
+    the launch sequence before copying out, so it returns that path's result,
+    and the next host call runs the persistent kernel again."""
+    rl = qm.ResidentLayer(seed=3, layer=0)
+    x = orc.fill_normal(13, 2048, 0.0, 1.0)
+    qm.set_fused(False)
+    want_seq = qm.moe_ffn_host(rl.c, x, 1)
+    qm.set_fused(True)
+    want_fused = run_layer(qm, rl, x, 1).reshape(-1)
+    n0 = qm.fused_recoveries()
+    qm.arm_test_abort(1)
+    got = qm.moe_ffn_host(rl.c, x, 1)
+    assert qm.fused_recoveries() == n0 + 1
+    assert np.array_equal(got.view(np.uint32), want_seq.view(np.uint32))
+    again = qm.moe_ffn_host(rl.c, x, 1)
+    assert qm.fused_recoveries() == n0 + 1
+    assert np.array_equal(again.view(np.uint32), want_fused.view(np.uint32))
+    with pytest.raises(qm.QmagError):
+        qm.check(qm.lib().qmag_moe_ffn_host(qm.C.byref(rl.c), None, None, 1))
+    rl.close()
