@@ -712,7 +712,12 @@ extern "C" int qmag_moe_ffn_host(const qmag_moe_layer *L, const float *x, float 
     std::lock_guard<std::mutex> guard(g_host_mu);
     hipStream_t s = ctx().stream;
     if (2 * half + 256 > g_host_pin_cap) {
-        if (g_host_pin) QMAG_HIP(hipHostFree(g_host_pin));   // no copy from it is pending: every call synchronises
+        if (g_host_pin) {
+            // a call that failed after queueing its copies returned without
+            // waiting for them: none may still read the buffer being freed
+            QMAG_HIP(hipStreamSynchronize(s));
+            QMAG_HIP(hipHostFree(g_host_pin));
+        }
         g_host_pin = nullptr;
         g_host_pin_cap = 0;
         QMAG_HIP(hipHostMalloc((void **)&g_host_pin, 2 * half + 256, hipHostMallocDefault));
