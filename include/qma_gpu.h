@@ -10,7 +10,10 @@
  *    run on the GPU (staged per calling thread) so a build that drops
  *    src/q8k.c and links this library keeps working unchanged; they are
  *    per-row calls and therefore latency-bound.  qma_q8k_available() reports
- *    whether a usable gfx950 device is present.
+ *    whether a usable gfx950 device is present; without one the other q8k
+ *    entries compute nothing and return zeros, as the reference's build
+ *    without dotprod does (q8k.c:280-316), and the quants.c entries abort
+ *    with a message (the reference has no unavailable form for them).
  *
  * 2. Device entries (qmag_*): the coarse seams of src/nn.c -- matmul
  *    (nn.c:307) and moe_ffn (nn.c:509) -- over weights resident in HBM in the

@@ -5,6 +5,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -438,6 +439,21 @@ static void ensure_ready_or_abort(const char *fn)
     if (!g_ctx.ready.load(std::memory_order_acquire) && qmag_init(0) != QMAG_OK) compat_abort(fn);
 }
 
+// No usable device: the q8k entries then do what the reference's build
+// without dotprod does (q8k.c:280-316: quant writes nothing, gateup gives
+// 0.0f, dot gives 0.0f), after one message on stderr.  The quants.c entries
+// have no such contract (the reference always computes them) and abort.
+static bool q8k_unavailable(const char *fn)
+{
+    if (g_ctx.ready.load(std::memory_order_acquire) || qmag_init(0) == QMAG_OK) return false;
+    static std::atomic<bool> said{false};
+    if (!said.exchange(true))
+        fprintf(stderr, "libqmagpu: %s called without a usable gfx950 device (%s); the q8k entries compute "
+                        "nothing and return zeros, as the reference's build without dotprod does; "
+                        "callers must check qma_q8k_available() first\n", fn, t_err);
+    return true;
+}
+
 static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 int qma_q8k_available(void)
@@ -448,7 +464,7 @@ int qma_q8k_available(void)
 
 void qma_q8k_quant(const float *x, int n, int8_t *xq, float *xd, int16_t *xsum)
 {
-    ensure_ready_or_abort("qma_q8k_quant");
+    if (q8k_unavailable("qma_q8k_quant")) return;
     if (n <= 0) return;
     const int nb = n / QK_K;
     const size_t ox = 0, oq = a256(sizeof(float) * (size_t)n), od = oq + a256((size_t)n),
@@ -500,7 +516,7 @@ float qma_q8k_dot(const void *row, int wtype, const int8_t *xq, const float *xd,
 {
     if (wtype != QMAG_TYPE_Q4_K && wtype != QMAG_TYPE_Q6_K) return 0.0f;   // q8k.c:314-315
     n -= n % QK_K;                     // whole super-blocks only, as q8k.c:92 (nb = n / QK_K)
-    if (n <= 0) return 0.0f;
+    if (n <= 0 || q8k_unavailable("qma_q8k_dot")) return 0.0f;
     float out = 0.0f;
     compat_dot(&row, 1, wtype, xq, xd, xsum, n, &out, "qma_q8k_dot");
     return out;
@@ -510,7 +526,7 @@ void qma_q8k_gateup(const void *g, const void *u, const int8_t *xq, const float 
                     const int16_t *xsum, int n, float *gate, float *up)
 {
     n -= n % QK_K;                     // whole super-blocks only (q8k.c:143)
-    if (n <= 0) {
+    if (n <= 0 || q8k_unavailable("qma_q8k_gateup")) {
         *gate = *up = 0.0f;
         return;
     }

@@ -52,3 +52,50 @@ def test_no_gpu_reports_unavailable(built):
     assert st == -3
     assert L.qma_q8k_available() == 0
     assert b"gfx950" in L.qmag_last_error() or b"device" in L.qmag_last_error()
+
+
+def test_no_gpu_q8k_entries_are_the_reference_stubs(built):
+    """Without a usable device the q8k entries do what the reference's build
+    without dotprod does (q8k.c:280-316): qma_q8k_quant writes nothing,
+    qma_q8k_gateup gives 0.0f twice, qma_q8k_dot gives 0.0f -- and the process
+    keeps running."""
+    import ctypes as C
+
+    import numpy as np
+    L = built.lib()
+    if L.qmag_init(0) == 0:
+        pytest.skip("a gfx950 GPU is visible")
+    n = 512
+    x = np.ones(n, np.float32)
+    xq = np.full(n, 7, np.int8)
+    xd = np.full(n // 256, 3.0, np.float32)
+    xs = np.full(n // 16, 5, np.int16)
+    p = lambda a: a.ctypes.data_as(C.c_void_p)
+    L.qma_q8k_quant(p(x), n, p(xq), p(xd), p(xs))
+    assert (xq == 7).all() and (xd == 3.0).all() and (xs == 5).all()
+    row = np.full(2 * 144, 0x11, np.uint8)
+    assert L.qma_q8k_dot(p(row), 12, p(xq), p(xd), p(xs), n) == 0.0
+    g, u = C.c_float(9.0), C.c_float(9.0)
+    L.qma_q8k_gateup(p(row), p(row), p(xq), p(xd), p(xs), n, C.byref(g), C.byref(u))
+    assert g.value == 0.0 and u.value == 0.0
+
+
+def test_no_gpu_f32_entries_abort_with_a_message(built):
+    """The quants.c entries have no unavailable form in the reference (it
+    always computes them), so without a device they abort with a message
+    rather than return a wrong value (run in a child process)."""
+    import subprocess
+    import sys
+    code = ("import ctypes as C, numpy as np, qmag\n"
+            "L = qmag.lib()\n"
+            "assert L.qmag_init(0) != 0\n"
+            "w = np.zeros(144, np.uint8); x = np.zeros(256, np.float32)\n"
+            "L.dot_q4_K_f32(w.ctypes.data_as(C.c_void_p), x.ctypes.data_as(C.c_void_p), 256)\n"
+            "print('returned')\n")
+    L = built.lib()
+    if L.qmag_init(0) == 0:
+        pytest.skip("a gfx950 GPU is visible")
+    env = dict(os.environ, PYTHONPATH=os.path.join(ROOT, "qwen-mobile-agent_amd"))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "returned" not in r.stdout
+    assert "dot_q4_K_f32 called without a usable gfx950 device" in r.stderr
