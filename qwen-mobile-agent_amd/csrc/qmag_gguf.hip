@@ -21,6 +21,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -206,7 +207,9 @@ int qmag_gguf_open(const char *path, qmag_gguf **out)
     if (alignment == 0 || alignment > 65536 || (alignment & (alignment - 1)))
         return fail_open(err(QMAG_ERR_ARG, "gguf: bad alignment %llu", (unsigned long long)alignment));
 
-    g->tensors.reserve((size_t)n_tensors);
+    // an entry takes at least 32 bytes of the file (name length, dims count,
+    // one dim, type, offset): a corrupt count reserves no more than that allows
+    g->tensors.reserve((size_t)std::min<uint64_t>(n_tensors, (uint64_t)(r.end - r.p) / 32));
     for (uint64_t i = 0; i < n_tensors && !r.bad; i++) {
         GgufTensor t;
         t.name = r.str();
