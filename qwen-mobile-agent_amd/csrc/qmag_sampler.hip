@@ -9,8 +9,9 @@
 //
 // One launch of one workgroup per 4096 logits.  Each workgroup applies the
 // penalty and the temperature to its logits and selects its k largest over
-// unique 64-bit keys (the value's order-preserving bits, then the
-// complemented index, so equal values order by ascending index): the value
+// unique 64-bit keys (the value's order-preserving bits with -0 folded into
+// +0, then the complemented index, so equal values order by ascending index,
+// and a bit that restores a zero's sign in the reported value): the value
 // half of the k-th largest of the threads' maxima bounds the answer from
 // below, and the few keys that reach it are sorted by one wave's bitonic
 // network (an exact radix select takes over when more than 128 reach it).
@@ -64,10 +65,20 @@ __device__ __forceinline__ float samp_val(uint32_t k)
 {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
-// unique selection key: value bits, then the complemented index
-__device__ __forceinline__ uint64_t samp_comp(uint32_t key, int id)
+// unique selection key: the value half, then the complemented index shifted
+// up one bit (ids are below 2^31, so the dropped top bit is 1 for all and the
+// order among ids is kept); the low bit is the sign of a zero value, which
+// the value half folds into +0 (the reference compares -0 and +0 as equal),
+// so it never decides an order and only restores the reported value
+__device__ __forceinline__ uint64_t samp_comp(uint32_t key, int id, float v)
 {
-    return ((uint64_t)key << 32) | (uint32_t)~(uint32_t)id;
+    const uint32_t neg_zero = __float_as_uint(v) == 0x80000000u ? 1u : 0u;
+    return ((uint64_t)key << 32) | ((uint32_t)~(uint32_t)id << 1) | neg_zero;
+}
+__device__ __forceinline__ int samp_id(uint64_t c) { return (int)~(((uint32_t)c >> 1) | 0x80000000u); }
+__device__ __forceinline__ float samp_value(uint64_t c)
+{
+    return (c & 1u) ? -0.0f : samp_val((uint32_t)(c >> 32));
 }
 
 // The value of lane (lane ^ m), m one of 1, 2, 4, 8, 16, 32 (a constant once
@@ -558,7 +569,7 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
 #pragma unroll
     for (int m = 0; m < SAMP_PER_THREAD; m++) {
         const int i = t + 256 * m;
-        c[m] = base + i < n ? samp_comp(samp_key(cv[m]), base + i) : 0ull;
+        c[m] = base + i < n ? samp_comp(samp_key(cv[m]), base + i, cv[m]) : 0ull;
     }
     const int valid = n - base < SAMP_CHUNK ? n - base : SAMP_CHUNK;
     const int kk = k < valid ? k : valid;
@@ -604,8 +615,8 @@ __global__ __launch_bounds__(256) void sampler_kernel(const float *__restrict__ 
         const int lane = t;
         uint64_t v = lane < k ? s_win[lane] : 0ull;
         if (!sorted) v = wave_sort64(v);
-        const int id = (int)~(uint32_t)v;
-        const float val = samp_val((uint32_t)(v >> 32));
+        const int id = samp_id(v);
+        const float val = samp_value(v);
         // results to pinned host memory with system-scope stores, waited for
         // before the completion marker is stored
         auto put = [&](int i, int v) { __hip_atomic_store(out + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); };

@@ -28,7 +28,12 @@ def _check_candidates(qm, orc, logits, kw, max_k):
     gi, gv = qm.sampler_candidates_dev(d.ptr, logits.size, sd, max_k)
     oi, ov = orc.sampler_candidates(logits, so, max_k)
     assert gi.size == oi.size
-    assert np.array_equal(gv.view(np.uint32), ov.view(np.uint32))
+    # values equal as the reference compares them (-0 == +0; without zeros
+    # this is bit equality), and every returned value is bit for bit its
+    # id's scaled logit, the sign of a zero included
+    assert np.array_equal(gv, ov)
+    sc = _scaled(orc, logits, kw)
+    assert np.array_equal(gv.view(np.uint32), sc[gi].view(np.uint32))
     if np.unique(ov).size == ov.size and (ov.size == 0 or np.count_nonzero(_scaled(orc, logits, kw) == ov[-1]) == 1):
         assert np.array_equal(gi, oi)
     else:
@@ -92,6 +97,24 @@ def test_candidates_ties(qm, orc):
     gi, gv = _check_candidates(qm, orc, logits, dict(temp=0.0, top_k=40, repeat_penalty=1.0), 40)
     boundary = gv[-1]
     assert list(gi[gv == boundary]) == list(np.flatnonzero(logits == boundary)[:np.count_nonzero(gv == boundary)])
+
+
+@pytest.mark.parametrize("temp", [1.0, 0.7, 0.0])
+def test_candidates_signed_zero_boundary(qm, orc, temp):
+    """The k-th value is zero, held by interleaved +0 and -0 logits: the
+    reference's comparisons treat them as one value, so the device orders
+    them by ascending id alone, and reports each one with its own sign."""
+    rng = np.random.default_rng(17)
+    n = 5000
+    logits = -np.abs(rng.standard_normal(n)).astype(np.float32) - 1.0
+    logits[rng.choice(n, 10, replace=False)] = 4.0 + rng.random(10).astype(np.float32)
+    zeros = rng.choice(n, 200, replace=False)
+    logits[zeros] = np.where(np.arange(200) % 3 == 0, np.float32(-0.0), np.float32(0.0))
+    gi, gv = _check_candidates(qm, orc, logits, dict(temp=temp, top_k=40, repeat_penalty=1.0), 40)
+    z = gi[gv == 0]
+    assert z.size == 40 - np.count_nonzero(logits > 0)
+    assert list(z) == list(np.flatnonzero(logits == 0)[:z.size])
+    assert np.any(np.signbit(gv[gv == 0])) and not np.all(np.signbit(gv[gv == 0]))
 
 
 def test_candidates_concentrated_chunk(qm, orc):
