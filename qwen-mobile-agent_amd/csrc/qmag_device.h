@@ -219,10 +219,16 @@ __device__ __forceinline__ int q8_round(float v)
     return q;
 }
 
+// |x| as an integer whose order is the order of the values: every NaN lies
+// above +Inf, so an integer maximum of these is the block's amax as
+// vmaxq_f32 finds it in q8k.c:46-52 (NaN as soon as one value is NaN, which
+// then gives d = 1, as amax > 0 is false); fmaxf would skip the NaN
+__device__ __forceinline__ int abs_bits(float v) { return (int)(__float_as_uint(v) & 0x7fffffffu); }
+
 __device__ __forceinline__ Q8Lane q8k_quant_lane(float4 v)
 {
-    float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    const float amax = group_max<64>(a);
+    const int a = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
+    const float amax = __int_as_float(group_max_i<64>(a));
     Q8Lane r;
     r.d = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / r.d;
@@ -255,9 +261,9 @@ __device__ __forceinline__ uint32_t q8_pack4(float4 v, float inv, int &sum)
 
 __device__ __forceinline__ Q8Lane2 q8k_quant_half(float4 a, float4 b)
 {
-    float m = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
-    m = fmaxf(m, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
-    const float amax = group_max<32>(m);
+    int m = max(max(abs_bits(a.x), abs_bits(a.y)), max(abs_bits(a.z), abs_bits(a.w)));
+    m = max(m, max(max(abs_bits(b.x), abs_bits(b.y)), max(abs_bits(b.z), abs_bits(b.w))));
+    const float amax = __int_as_float(group_max_i<32>(m));
     Q8Lane2 r;
     r.d = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / r.d;

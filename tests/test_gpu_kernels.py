@@ -48,6 +48,34 @@ def test_q8k_ties_and_spikes(qm, orc):
     assert xd.download(np.float32)[0] == 1.0
 
 
+def test_q8k_special_values(qm, orc):
+    """Blocks with NaN (alone, all, beside +Inf), +-Inf, subnormal values,
+    amax/127 underflowing to 0, tiny, near-overflow and the largest finite
+    values, +0 and -0: bytes, scales and sums bit for bit the oracle's (which
+    a CPU test pins to the NEON instructions' definitions: a NaN anywhere in
+    a block makes amax NaN and so d = 1).  The one-launch T = 1 matmul, which
+    quantises x in LDS, gives the two-step form's outputs on the same x."""
+    from test_oracle_q8k import special_blocks
+    blocks = special_blocks()
+    x = np.concatenate(list(blocks.values()))
+    n = x.size
+    xb, xq, xd, xs = _q8_dev(qm, x, n, 1)
+    gq, gd, gs = xq.download(np.int8), xd.download(np.float32), xs.download(np.int16)
+    oq, od, os_ = orc.q8k_quant(x)
+    for i, kind in enumerate(blocks):
+        assert np.array_equal(gq[256 * i:256 * (i + 1)], oq[256 * i:256 * (i + 1)]), kind
+        assert gd.view(np.uint32)[i] == od.view(np.uint32)[i], kind
+        assert np.array_equal(gs[16 * i:16 * (i + 1)], os_[16 * i:16 * (i + 1)]), kind
+    n_mv = 4096                                      # the first 16 blocks: a tiled one-launch instance
+    W = qm.DBuf.from_array(orc.quantize_q4k(orc.fill_normal(3, n_mv * 64, 0.0, 0.02)))
+    o1, o2 = qm.DBuf(4 * 64), qm.DBuf(4 * 64)
+    x16 = qm.DBuf.from_array(np.resize(x, n_mv).astype(np.float32))
+    _, q16, d16, s16 = _q8_dev(qm, np.resize(x, n_mv), n_mv, 1)
+    qm.matmul_dev(x16, W, n_mv, 64, 1, 12, o1)
+    qm.matmul_q8k_dev(q16, d16, s16, W, n_mv, 64, 1, 12, o2)
+    assert np.array_equal(o1.download(np.float32), o2.download(np.float32), equal_nan=True)
+
+
 def _exact_q4k_rows(rng, n_out, nb):
     """Blocks with d = 1, dmin = 1 (fp16), random 6-bit scales/mins and
     nibbles: with xd = 1 every row dot is an integer below 2^24, so the fp32

@@ -175,3 +175,72 @@ def test_matmul_driver_rows(orc):
                         for r in range(n_out)]
                 assert np.array_equal(out[t], np.array(want, dtype=np.float32))
     orc.set_threads(1)
+
+
+def special_blocks():
+    """Blocks of special values, each 256 long: a NaN among finite values,
+    all NaN, NaN beside +Inf, +Inf, -Inf, subnormal values (amax/127 still
+    subnormal), values so small that amax/127 underflows to 0, tiny normal
+    values, near-overflow values, the largest finite values, +0 and -0."""
+    rng = np.random.default_rng(5)
+    f = np.float32
+    out = {}
+    for kind in ("nan", "allnan", "nan_inf", "pinf", "ninf", "sub", "underflow", "tiny", "huge", "max",
+                 "zero", "negzero"):
+        x = rng.standard_normal(256).astype(f)
+        if kind == "nan":
+            x[17] = np.nan
+        elif kind == "allnan":
+            x[:] = np.nan
+        elif kind == "nan_inf":
+            x[3], x[9] = np.inf, np.nan
+        elif kind == "pinf":
+            x[3] = np.inf
+        elif kind == "ninf":
+            x[200] = -np.inf
+        elif kind == "sub":
+            x = (x * f(1e-40)).astype(f)
+        elif kind == "underflow":
+            x = (x * f(1e-44)).astype(f)
+        elif kind == "tiny":
+            x = (x * f(1e-36)).astype(f)
+        elif kind == "huge":
+            x = (x * f(1e37)).astype(f)
+        elif kind == "max":
+            x[5], x[6] = f(3.4028235e38), -f(3.4028235e38)
+        elif kind == "zero":
+            x[:] = 0.0
+        elif kind == "negzero":
+            x[:] = -0.0
+        out[kind] = x
+    return out
+
+
+def neon_q8k_block(x):
+    """quantize_row_q8k for one block by the NEON instructions' definitions
+    (q8k.c:41-80): vmaxq_f32 / vmaxvq_f32 return NaN when an operand is NaN;
+    s = amax/127 unless !(amax > 0), then 1; vcvtaq_s32_f32 rounds half away
+    from zero, saturates to int32 and gives 0 for NaN; then the clamp to
+    +-127 and the 16-lane sums."""
+    a = np.abs(x.astype(np.float32))
+    amax = np.float32(np.nan) if np.isnan(a).any() else np.float32(max(0.0, float(a.max())))
+    s = amax / np.float32(127.0) if amax > 0 else np.float32(1.0)
+    inv = np.float32(1.0) / np.float32(s)
+    v = (x.astype(np.float32) * inv).astype(np.float64)
+    r = np.where(np.isnan(v), 0.0, np.sign(v) * np.floor(np.abs(v) + 0.5))
+    q = np.clip(np.clip(r, -2.0 ** 31, 2.0 ** 31 - 1), -127, 127).astype(np.int8)
+    return q, np.float32(s), q.astype(np.int32).reshape(16, 16).sum(axis=1).astype(np.int16)
+
+
+def test_q8k_special_values_follow_neon_semantics(orc):
+    for kind, x in special_blocks().items():
+        with np.errstate(over="ignore", invalid="ignore"):
+            eq, ed, es = neon_q8k_block(x)
+        q, d, s = orc.q8k_quant(x)
+        assert np.array_equal(q, eq), kind
+        assert d.view(np.uint32)[0] == np.array([ed], np.float32).view(np.uint32)[0], kind
+        assert np.array_equal(s, es), kind
+    # the cases that pin the NaN rule: a NaN gives d = 1, x itself rounded
+    x = special_blocks()["nan"]
+    q, d, _ = orc.q8k_quant(x)
+    assert d[0] == 1.0 and q[17] == 0 and q[0] == np.clip(np.round(x[0]), -127, 127)
