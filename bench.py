@@ -46,18 +46,28 @@ METRIC = "MoE FFN decode tokens/s + achieved HBM GB/s (% of peak), Q4_K/Q6_K, 1 
 # HBM bytes per launch of the fused decode kernel, from two rocprofv3 counter
 # passes over bench.py (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors
 # read off a 1 GiB copy kernel in the same runs), with the profile holding
-# them and the SHA-256 (first 16 hex digits) of the kernel source they were
-# taken on.  The figure is reported only while that source is unchanged: an
-# edit to the kernel needs new counter passes (and a new entry here).
-FUSED_TRAFFIC = {"bytes": 869.3e6, "profile": "profiles/moe_decode_kernel_c4_hbm_counters.md",
-                 "source": "qwen-mobile-agent_amd/csrc/qmag_fused.hip", "source_sha16": "106a7a3453061ea3"}
+# them and the SHA-256 (first 16 hex digits) of the kernel's sources they were
+# taken on: the kernel file and the headers it is compiled with, hashed in
+# this order.  The figure is reported only while those sources are unchanged:
+# an edit needs new counter passes (and a new entry here).
+FUSED_TRAFFIC = {"bytes": 869.1e6, "profile": "profiles/moe_decode_kernel_c4_hbm_counters.md",
+                 "sources": ["qwen-mobile-agent_amd/csrc/qmag_fused.hip", "qwen-mobile-agent_amd/csrc/qmag_device.h",
+                             "qwen-mobile-agent_amd/csrc/qmag_internal.h"],
+                 "source_sha16": "7c2357cb90829832"}
+
+
+def fused_source_sha16():
+    h = hashlib.sha256()
+    for rel in FUSED_TRAFFIC["sources"]:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
 
 
 def fused_traffic() -> tuple:
     """(HBM bytes per decode launch or None, where the figure comes from)."""
     try:
-        with open(os.path.join(ROOT, FUSED_TRAFFIC["source"]), "rb") as f:
-            sha = hashlib.sha256(f.read()).hexdigest()[:16]
+        sha = fused_source_sha16()
     except OSError:
         sha = None
     same = sha == FUSED_TRAFFIC["source_sha16"]
