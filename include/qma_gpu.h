@@ -50,11 +50,15 @@ extern "C" {
 #define QMAG_ERR_REPLAYED (-5) /* decode calls were re-run after an expired
                                   wait; work queued after them (logits) is
                                   stale and must be queued again            */
-/* Buffers passed to the device entries must stay valid until the next
-   qmag_sync or qmag_d2h: the library may re-run the calls issued since the
-   previous one (see qmag_fused_recoveries).  Only those MoE calls are re-run:
-   other device work queued after them that read their outputs (an LM-head
-   matmul, say) is re-queued by the caller when qmag_fused_recoveries rises. */
+/* Buffers passed to the MoE device entries must stay allocated, and the
+   input of an out-of-place call (x != out) must keep its contents, until the
+   next qmag_sync, qmag_d2h, sampler or host-buffer call, which checks for an
+   expired wait: the library may re-run the calls issued since the previous
+   check (see qmag_fused_recoveries), reading those inputs again.  The input
+   of an in-place call (a stack, or x == out) is copied by the library before
+   the call and needs no such care.  Only those MoE calls are re-run: other
+   device work queued after them that read their outputs (an LM-head matmul,
+   say) is re-queued by the caller when qmag_fused_recoveries rises. */
 
 /* ------------------------------------------------------------------------ */
 /* Reference-compatible entries                                              */
