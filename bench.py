@@ -50,10 +50,10 @@ METRIC = "MoE FFN decode tokens/s + achieved HBM GB/s (% of peak), Q4_K/Q6_K, 1 
 # taken on: the kernel file and the headers it is compiled with, hashed in
 # this order.  The figure is reported only while those sources are unchanged:
 # an edit needs new counter passes (and a new entry here).
-FUSED_TRAFFIC = {"bytes": 869.1e6, "profile": "profiles/moe_decode_kernel_c4_hbm_counters.md",
+FUSED_TRAFFIC = {"bytes": 869.4e6, "profile": "profiles/moe_decode_kernel_c4_hbm_counters.md",
                  "sources": ["qwen-mobile-agent_amd/csrc/qmag_fused.hip", "qwen-mobile-agent_amd/csrc/qmag_device.h",
                              "qwen-mobile-agent_amd/csrc/qmag_internal.h"],
-                 "source_sha16": "7c2357cb90829832"}
+                 "source_sha16": "4b9c5003ac8317ef"}
 
 
 def fused_source_sha16():

@@ -248,7 +248,8 @@ int qmag_dequant_dev(const void *W, int wtype, int64_t n, float *y);
 /* The fp32 dequantise-then-dot matmul (dot_q4_K_f32 / dot_q6_K_f32 per row,
    src/quants.c:80-133; the QMA_NOQ8K path, nn.c:393-407, 475-492):
    out[t][r] = sum_i deq(W_r)_i * x[t][i], no activation quantisation.
-   n_in: a multiple of 256 up to 8192. */
+   n_in: any multiple of 256 (rows longer than 8192 values are taken in
+   8192-value chunks whose partial sums are added in chunk order). */
 int qmag_matmul_f32_dev(const float *x, const void *W, int n_in, int n_out, int T, int wtype,
                         float *out);
 

@@ -50,6 +50,7 @@ enum WsSlot {
     WS_XMB,                         // grouped prefill: Q8_K(x) sub-block sums times the block scale
     WS_SAMP,                        // sampler: per-chunk candidates and the merged list
     WS_HOSTIO,                      // qmag_moe_ffn_host: the device copies of x and out
+    WS_F32PART,                     // fp32 matmul rows longer than one LDS chunk: per-chunk partials
     WS_COUNT
 };
 void *workspace(int slot, size_t bytes, int *status);

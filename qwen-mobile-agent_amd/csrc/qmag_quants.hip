@@ -79,21 +79,23 @@ int launch_dequant(const void *W, int wtype, long n, float *y, hipStream_t s)
 // ------------------------------------------------------ fp32 matvec ----
 // out[t][r] = sum_i deq(W[r])_i * x[t][i].  x of one token sits in LDS; a row
 // is split into 64-value tasks (f32_task) spread over LPR lanes, each lane
-// looping over its tasks.  Grid: (row chunks, T).
+// looping over its tasks.  Grid: (row chunks, T).  A launch covers nb
+// super-blocks of each row: the whole row, or for rows longer than the LDS
+// chunk one chunk of it (x_stride and rb then give the full rows' strides).
 constexpr int F32_MAX_IN = 8192;
 
 template <int WT, int LPR>
 __global__ __launch_bounds__(256) void f32dot_kernel(const uint8_t *__restrict__ W, const float *__restrict__ x,
-                                                     float *__restrict__ out, int nb, int n_out)
+                                                     float *__restrict__ out, int nb, int n_out, int x_stride,
+                                                     size_t rb)
 {
     __shared__ __align__(16) float s_x[F32_MAX_IN];
     const int t = (int)blockIdx.y;
     const int n_in = nb * QK_K;
-    const float *xt = x + (size_t)t * n_in;
+    const float *xt = x + (size_t)t * x_stride;
     for (int i = (int)threadIdx.x; i < n_in / 4; i += (int)blockDim.x)
         ((float4 *)s_x)[i] = ldg4(xt + 4 * i);
     __syncthreads();
-    const size_t rb = (size_t)nb * (WT == QMAG_TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES);
     const int lane = lane_id(), sub = lane % LPR;
     const int rows_per_wave = 64 / LPR;
     const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
@@ -110,7 +112,8 @@ __global__ __launch_bounds__(256) void f32dot_kernel(const uint8_t *__restrict__
 }
 
 template <int WT>
-static int launch_f32dot_t(const float *x, const void *W, int nb, int n_out, int T, float *out, hipStream_t s)
+static int launch_f32dot_t(const float *x, const void *W, int nb, int n_out, int T, float *out, hipStream_t s,
+                           int x_stride, size_t rb)
 {
     const int ntask = 4 * nb;
     const int lpr = ntask >= 64 ? 64 : ntask > 16 ? 32 : ntask > 8 ? 16 : ntask > 4 ? 8 : 4;
@@ -121,26 +124,58 @@ static int launch_f32dot_t(const float *x, const void *W, int nb, int n_out, int
     const dim3 grid((unsigned)wgs, (unsigned)T);
     const uint8_t *w = (const uint8_t *)W;
     switch (lpr) {
-    case 4: hipLaunchKernelGGL((f32dot_kernel<WT, 4>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
-    case 8: hipLaunchKernelGGL((f32dot_kernel<WT, 8>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
-    case 16: hipLaunchKernelGGL((f32dot_kernel<WT, 16>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
-    case 32: hipLaunchKernelGGL((f32dot_kernel<WT, 32>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
-    default: hipLaunchKernelGGL((f32dot_kernel<WT, 64>), grid, dim3(256), 0, s, w, x, out, nb, n_out); break;
+    case 4: hipLaunchKernelGGL((f32dot_kernel<WT, 4>), grid, dim3(256), 0, s, w, x, out, nb, n_out, x_stride, rb); break;
+    case 8: hipLaunchKernelGGL((f32dot_kernel<WT, 8>), grid, dim3(256), 0, s, w, x, out, nb, n_out, x_stride, rb); break;
+    case 16: hipLaunchKernelGGL((f32dot_kernel<WT, 16>), grid, dim3(256), 0, s, w, x, out, nb, n_out, x_stride, rb); break;
+    case 32: hipLaunchKernelGGL((f32dot_kernel<WT, 32>), grid, dim3(256), 0, s, w, x, out, nb, n_out, x_stride, rb); break;
+    default: hipLaunchKernelGGL((f32dot_kernel<WT, 64>), grid, dim3(256), 0, s, w, x, out, nb, n_out, x_stride, rb); break;
     }
     QMAG_HIP(hipGetLastError());
     return QMAG_OK;
 }
 
+// out[i] = part[0][i] + part[1][i] + ... in chunk order, from 0.0f: the order
+// in which the host-pointer entries add their chunks
+__global__ __launch_bounds__(256) void f32_chunk_sum_kernel(const float *__restrict__ part, int nch, long n,
+                                                            float *__restrict__ out)
+{
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        float v = 0.0f;
+        for (int c = 0; c < nch; c++) v += part[(size_t)c * n + i];
+        out[i] = v;
+    }
+}
+
 int launch_f32dot(const float *x, const void *W, int n_in, int n_out, int T, int wtype, float *out,
                   hipStream_t s)
 {
-    if (n_in <= 0 || n_in % QK_K || n_in > F32_MAX_IN || n_out <= 0 || T <= 0 || T > 65535)
-        return fail(QMAG_ERR_ARG, "f32 matvec: n_in=%d (multiple of 256, <= %d) n_out=%d T=%d", n_in,
-                    F32_MAX_IN, n_out, T);
+    if (n_in <= 0 || n_in % QK_K || n_out <= 0 || T <= 0 || T > 65535)
+        return fail(QMAG_ERR_ARG, "f32 matvec: n_in=%d (a multiple of 256) n_out=%d T=%d", n_in, n_out, T);
     if (!x || !W || !out) return fail(QMAG_ERR_ARG, "f32 matvec: null pointer");
-    if (wtype == QMAG_TYPE_Q4_K) return launch_f32dot_t<QMAG_TYPE_Q4_K>(x, W, n_in / QK_K, n_out, T, out, s);
-    if (wtype == QMAG_TYPE_Q6_K) return launch_f32dot_t<QMAG_TYPE_Q6_K>(x, W, n_in / QK_K, n_out, T, out, s);
-    return fail(QMAG_ERR_ARG, "f32 matvec: unsupported wtype %d", wtype);
+    if (wtype != QMAG_TYPE_Q4_K && wtype != QMAG_TYPE_Q6_K)
+        return fail(QMAG_ERR_ARG, "f32 matvec: unsupported wtype %d", wtype);
+    const size_t bb = wtype == QMAG_TYPE_Q4_K ? Q4K_BYTES : Q6K_BYTES, rb = (size_t)(n_in / QK_K) * bb;
+    auto launch = [&](const float *xc, const uint8_t *wc, int nbc, float *o) {
+        return wtype == QMAG_TYPE_Q4_K ? launch_f32dot_t<QMAG_TYPE_Q4_K>(xc, wc, nbc, n_out, T, o, s, n_in, rb)
+                                       : launch_f32dot_t<QMAG_TYPE_Q6_K>(xc, wc, nbc, n_out, T, o, s, n_in, rb);
+    };
+    if (n_in <= F32_MAX_IN) return launch(x, (const uint8_t *)W, n_in / QK_K, out);
+    // longer rows: one launch per chunk of F32_MAX_IN values into partials,
+    // then their sum in chunk order
+    const int nch = (n_in + F32_MAX_IN - 1) / F32_MAX_IN;
+    const size_t n = (size_t)T * n_out;
+    int st = QMAG_OK;
+    float *part = (float *)workspace(WS_F32PART, sizeof(float) * n * (size_t)nch, &st);
+    if (!part) return st;
+    for (int c = 0; c < nch; c++) {
+        const int c0 = c * F32_MAX_IN, cn = n_in - c0 < F32_MAX_IN ? n_in - c0 : F32_MAX_IN;
+        st = launch(x + c0, (const uint8_t *)W + (size_t)(c0 / QK_K) * bb, cn / QK_K, part + (size_t)c * n);
+        if (st) return st;
+    }
+    const long wgs = (long)((n + 255) / 256) < 4096 ? (long)((n + 255) / 256) : 4096;
+    hipLaunchKernelGGL(f32_chunk_sum_kernel, dim3((unsigned)wgs), dim3(256), 0, s, part, nch, (long)n, out);
+    QMAG_HIP(hipGetLastError());
+    return QMAG_OK;
 }
 
 }  // namespace qmag

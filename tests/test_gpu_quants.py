@@ -111,10 +111,12 @@ def test_q8k_dot_subnormal_scales(qm, orc):
 
 @pytest.mark.parametrize("wtype", [12, 14])
 @pytest.mark.parametrize("n_in,n_out,T", [(256, 100, 1), (2048, 512, 1), (512, 2048, 3), (8192, 64, 2),
-                                          (768, 77, 1)])
+                                          (768, 77, 1), (12288, 40, 3), (16640, 33, 2), (24576, 17, 1)])
 def test_matmul_f32_dev(qm, orc, wtype, n_in, n_out, T):
     """The QMA_NOQ8K dequantise-then-dot path against the oracle's
-    dot_q4_K_f32 / dot_q6_K_f32 per row (quants.c:80-133)."""
+    dot_q4_K_f32 / dot_q6_K_f32 per row (quants.c:80-133), including rows
+    longer than one 8192-value LDS chunk (a whole number of chunks, a
+    ragged last chunk), whose partial sums are added in chunk order."""
     W = orc.quantize(orc.fill_normal(500 + n_in + n_out, n_in * n_out, 0.0, 0.02), wtype)
     x = orc.fill_normal(600 + T, T * n_in, 0.0, 1.0)
     out = qm.DBuf(4 * T * n_out)
