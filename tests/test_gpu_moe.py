@@ -936,3 +936,47 @@ def test_moe_ffn_host_recovers_expired_wait(qm, orc):
     with pytest.raises(qm.QmagError):
         qm.check(qm.lib().qmag_moe_ffn_host(qm.C.byref(rl.c), None, None, 1))
     rl.close()
+
+
+def test_grouped_prefill_random_large_batches(qm, orc):
+    """Seeded random layers through the grouped prefill at T from 65 to 300
+    (buckets of many 64-pair chunks, partial chunks of every size, biased and
+    unbiased routers): every token's selection checked as check_selection
+    does, every 16th token teacher-forced stage by stage (h per slot, then the
+    output from the GPU's h through the oracle's down projection and
+    combine)."""
+    rng = np.random.default_rng(4242)
+    qm.set_grouped(True)
+    for case in range(3):
+        N = int(rng.choice([256, 512, 1024])); F = int(rng.choice([256, 512, 1024]))
+        E = int(rng.integers(16, 129)); K = int(rng.integers(1, 9)); T = int(rng.integers(65, 301))
+        td, tds = int(rng.choice([12, 14])), int(rng.choice([12, 14]))
+        bias = None if case == 0 else float(case)
+        hl = make_host_layer(orc, 5000 + case, N, F, E, K, td, router_bias_std=bias, t_down_sh=tds)
+        rl = qm.ResidentLayer.from_host(hl)
+        x = orc.fill_normal(5100 + case, T * N, 0.0, 1.0)
+        got = run_layer(qm, rl, x, T)
+        st = qm.moe_last_stage(E, K, F, n_tok=T)
+        gb, db = hl.gate_exps.size // E, hl.down_exps.size // E
+        for t in range(T):
+            xt = x[t * N:(t + 1) * N]
+            sel_o, w_o, lg_o = orc.moe_route(hl, xt)
+            assert max_rel_err(st["logits"][t], lg_o) < TOL, (case, t)
+            check_selection(st["sel"][t], st["w"][t], sel_o, w_o, lg_o, K, f"case {case} token {t}")
+            if t % 16:
+                continue
+            xq, xd, xs = orc.q8k_quant(xt)
+            acc = np.zeros(N, np.float32)
+            for s in range(K + 1):
+                if s < K:
+                    e = int(st["sel"][t][s])
+                    ge, ue = hl.gate_exps[e * gb:(e + 1) * gb], hl.up_exps[e * gb:(e + 1) * gb]
+                    dn, wt, scale = hl.down_exps[e * db:(e + 1) * db], hl.t_down_exps, st["w"][t][s]
+                else:
+                    ge, ue = hl.gate_shexp, hl.up_shexp
+                    dn, wt, scale = hl.down_shexp, hl.t_down_shexp, st["gs"][t]
+                assert max_rel_err(st["h"][t][s], orc.moe_expert_h(ge, ue, N, F, xq, xd, xs)) < TOL, (case, t, s)
+                y = orc.matmul_q8k(st["h"][t][s], dn, F, N, 1, wt)[0]
+                acc = (acc + (np.float32(scale) * y).astype(np.float32)).astype(np.float32)
+            assert max_rel_err(got[t], acc) < TOL, (case, t)
+        rl.close()

@@ -394,3 +394,44 @@ def test_matmul_group_rejects_bad_arguments(qm):
     assert call(2048, 1, n_out=0) == -2
     assert call(1024, 1, wtype=270) == -2
     assert call(2048, 2) == 0
+
+
+def test_matmul_random_shapes_vs_oracle(qm, orc):
+    """Seeded random shapes through the matmul seam: row lengths of 1-48
+    super-blocks (powers of two take the tiled kernels, the others the
+    per-row one), 1-3,000 rows, T 1-8, Q4_K, Q6_K and repacked Q6_K rows,
+    the one-launch x form, the pre-quantised Q8_K form and the fp32 form,
+    each within 1e-4 of the oracle per token."""
+    rng = np.random.default_rng(77)
+    for case in range(24):
+        k = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 12, 16, 17, 24, 32, 33, 48]))
+        n_in = 256 * k
+        n_out = int(rng.integers(1, min(3000, (1 << 22) // n_in) + 1))
+        T = int(rng.choice([1, 1, 2, 3, 5, 8]))
+        wt = int(rng.choice([12, 14, qm.TYPE_Q6_K_R])) if n_in % 2048 == 0 else int(rng.choice([12, 14]))
+        form = str(rng.choice(["x", "q8k"] if wt == qm.TYPE_Q6_K_R else ["x", "q8k", "f32"]))
+        wo = 14 if wt == qm.TYPE_Q6_K_R else wt
+        Wh = orc.quantize(orc.fill_normal(900 + case, n_in * n_out, 0.0, 0.02), wo)
+        x = orc.fill_normal(950 + case, T * n_in, 0.0, 1.0)
+        W = qm.DBuf.from_array(Wh)
+        if wt == qm.TYPE_Q6_K_R:
+            qm.repack_q6k_dev(W, W, n_in, n_out)
+        xb, out = qm.DBuf.from_array(x), qm.DBuf(4 * T * n_out)
+        if form == "x":
+            qm.matmul_dev(xb, W, n_in, n_out, T, wt, out)
+        elif form == "q8k":
+            xq, xd, xs = qm.DBuf(T * n_in), qm.DBuf(4 * T * n_in // 256), qm.DBuf(2 * T * n_in // 16)
+            qm.q8k_quant_dev(xb, n_in, T, xq, xd, xs)
+            qm.matmul_q8k_dev(xq, xd, xs, W, n_in, n_out, T, wt, out)
+        else:
+            qm.matmul_f32_dev(xb, W, n_in, n_out, T, wt, out)
+        got = out.download(np.float32).reshape(T, n_out)
+        if form == "f32":
+            rb = Wh.size // n_out
+            ref = np.array([[orc.dot_f32(Wh[r * rb:(r + 1) * rb], wo, x[t * n_in:(t + 1) * n_in], n_in)
+                             for r in range(n_out)] for t in range(T)], np.float32)
+        else:
+            ref = orc.matmul_q8k(x, Wh, n_in, n_out, T, wo).reshape(T, n_out)
+        for t in range(T):
+            assert max_rel_err(got[t], ref[t]) < TOL, (case, n_in, n_out, T, wt, form, t)
+        W.close()

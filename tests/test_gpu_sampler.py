@@ -230,3 +230,56 @@ def test_sample_after_recovery_reports_stale_logits(qm, orc):
     assert gt == orc.sampler_pick(so, oi, ov, 0.9)
     assert sd.seed == so.seed and sd.n_last == so.n_last == 1
     rl.close()
+
+
+def test_sampling_random_parameters_vs_oracle(qm, orc):
+    """Seeded random sampler states and logits: vocabularies of 1-20,000
+    (and a few up to the 151,936 of the LM head), temperatures 0-1.7, top_k
+    0-100 against max_k 1-64, top_p 0.05-1, repeat penalties below and above
+    1 over histories with repeats and ids out of range; logits normal, tied
+    (rounded, with +0 and -0), largely masked at -1e30, partly -inf, or
+    wide.  Candidates as _check_candidates requires; when the candidate
+    values are all distinct, the pick, seed and history equal the oracle's
+    over four steps."""
+    rng = np.random.default_rng(2025)
+    for case in range(120):
+        n = int(rng.integers(1, 200)) if case % 3 == 0 else int(rng.integers(200, 20000))
+        if case % 40 == 39:
+            n = V
+        kind = str(rng.choice(["normal", "ties", "masked", "neginf", "wide"]))
+        kw = dict(seed=int(rng.integers(1, 1 << 62)), temp=float(rng.choice([0.0, 0.2, 0.7, 1.0, 1.7])),
+                  top_k=int(rng.choice([0, 1, 5, 20, 40, 64, 100])), top_p=float(rng.choice([0.05, 0.5, 0.9, 1.0])),
+                  repeat_penalty=float(rng.choice([1.0, 1.1, 1.3, 0.8])))
+        max_k = int(rng.choice([1, 8, 20, 40, 64]))
+        last = [int(v) for v in rng.integers(-5, n + 5, int(rng.integers(0, 81)))]
+        sd, so = _state(qm, orc, last=last, **kw)
+        d = qm.DBuf(4 * n)
+        for step in range(4):
+            if kind == "normal":
+                lg = (rng.standard_normal(n) * 2.5).astype(np.float32)
+            elif kind == "ties":
+                lg = np.round(rng.standard_normal(n) * 3).astype(np.float32)
+            elif kind == "masked":
+                lg = (rng.standard_normal(n) * 2).astype(np.float32)
+                lg[rng.random(n) < 0.95] = -1e30
+            elif kind == "neginf":
+                lg = (rng.standard_normal(n) * 2).astype(np.float32)
+                lg[rng.random(n) < 0.3] = -np.inf
+            else:
+                lg = (rng.standard_normal(n) * 200).astype(np.float32)
+            d.upload(lg)
+            gi, gv = qm.sampler_candidates_dev(d.ptr, n, sd, max_k)
+            oi, ov = orc.sampler_candidates(lg, so, max_k)
+            kwc = dict(kw, last=list(so.last_tokens)[:so.n_last])
+            assert gi.size == oi.size and np.array_equal(gv, ov), (case, step)
+            sc = _scaled(orc, lg, kwc)
+            assert np.array_equal(gv.view(np.uint32), sc[gi].view(np.uint32)), (case, step)
+            if np.unique(ov).size == ov.size and (ov.size == 0 or np.count_nonzero(sc == ov[-1]) == 1):
+                assert np.array_equal(gi, oi), (case, step)
+            if np.unique(ov).size != ov.size:
+                continue                 # the pick among equal values follows each side's order
+            gt = qm.sampler_sample_dev(d.ptr, n, sd, max_k, kw["top_p"])
+            ot = orc.sampler_pick(so, oi, ov, kw["top_p"])
+            assert gt == ot and sd.seed == so.seed and sd.n_last == so.n_last, (case, step)
+            assert list(sd.last_tokens)[:sd.n_last] == list(so.last_tokens)[:so.n_last], (case, step)
+        d.close()
