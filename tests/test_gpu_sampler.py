@@ -78,10 +78,11 @@ def test_candidates_vs_oracle(qm, orc, temp, top_k, max_k, rp):
     assert gi.size == min(max(top_k, 1), max_k)
 
 
-@pytest.mark.parametrize("n", [1, 3, 63, 64, 1000, 1024, 4095, 4097, 8191, 128 * 4096])
+@pytest.mark.parametrize("n", [1, 3, 63, 64, 1000, 1024, 4095, 4097, 8191, 248320, 128 * 4096])
 def test_candidates_vocab_edges(qm, orc, n):
     """Ragged vocabularies: k clamps to n_vocab (sampler.c:63-66), the last
-    chunk is partial, the largest vocabulary the device merge takes."""
+    chunk is partial, the engine's own vocabulary (N_VOCAB, qma.h:33: 60 full
+    chunks and one of 2,560), the largest vocabulary the device merge takes."""
     rng = np.random.default_rng(n)
     logits = rng.standard_normal(n).astype(np.float32)
     for top_k, max_k in ((40, 40), (64, 64), (1, 40)):
