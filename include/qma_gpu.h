@@ -19,7 +19,11 @@
  *    (nn.c:307) and moe_ffn (nn.c:509) -- over weights resident in HBM in the
  *    GGUF block layout.  All pointers are device pointers, work is ordered on
  *    the library stream, and each returns an int status (0 ok, <0 error;
- *    qmag_last_error() gives the text).
+ *    qmag_last_error() gives the text).  They are called from one host thread
+ *    at a time, as the engine calls its seams (from qma_eval on the main
+ *    thread, nn.c:2111-2286): they share the stream, workspaces and the
+ *    recovery log.  The group 1 entries and the expert cache may be called
+ *    from several threads at once.
  *
  * Weight formats: GGML Q4_K (type 12, 144-byte super-blocks) and Q6_K
  * (type 14, 210-byte super-blocks), src/qma.h:67-90.  Activation Q8_K is the
