@@ -126,6 +126,9 @@ __global__ __launch_bounds__(512) void router_tile_kernel(const float *__restric
 // first, then the partial ones by decreasing size, so the longest
 // workgroups start first and the grid ends on the shortest ones.
 constexpr int MC = 64;            // pairs per chunk of the chunked GEMMs (4 MFMA tiles)
+// the GEMM workgroups' 4 waves read 16 of a chunk's pair ids each, and the
+// group kernel's chunk scans run within one wave: a chunk is 4 x 16 pairs
+static_assert(MC == 4 * 16 && MC <= 64, "chunk size is tied to the 4-wave id loads");
 
 __global__ __launch_bounds__(1024) void group_kernel(const int *__restrict__ sel, int T, int K, int E,
                                                      int *__restrict__ grp,
