@@ -99,3 +99,37 @@ def test_no_gpu_f32_entries_abort_with_a_message(built):
     r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode != 0 and "returned" not in r.stdout
     assert "dot_q4_K_f32 called without a usable gfx950 device" in r.stderr
+
+
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_header_compiles_alone(lang, tmp_path):
+    """qma_gpu.h is valid C99 and C++ on its own (an engine includes it from
+    C; a C++ caller gets extern "C" linkage)."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc" if lang == "c" else "g++")
+    if not cc:
+        pytest.skip("no host compiler")
+    src = tmp_path / ("h.c" if lang == "c" else "h.cpp")
+    src.write_text('#include "qma_gpu.h"\nint main(void) { return qmag_init(0) == 0 ? 0 : 1; }\n')
+    std = "-std=c99" if lang == "c" else "-std=c++17"
+    r = subprocess.run([cc, std, "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-I", os.path.join(ROOT, "include"),
+                        str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_header_compiles_after_the_engine_header(tmp_path):
+    """Included after the engine's own qma.h (where the reference tree is
+    present), the header adds no conflicting declaration: the compatible
+    entries' prototypes are the engine's, and the quants.c ones are skipped
+    in favour of the engine's typed ones."""
+    import shutil
+    import subprocess
+    ref = "/root/reference/src"
+    if not os.path.exists(os.path.join(ref, "qma.h")) or not shutil.which("gcc"):
+        pytest.skip("the engine's header is not available here")
+    src = tmp_path / "both.c"
+    src.write_text('#include "qma.h"\n#include "qma_gpu.h"\nint main(void) { return qma_q8k_available(); }\n')
+    r = subprocess.run(["gcc", "-std=gnu11", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-I", ref, "-I",
+                        os.path.join(ROOT, "include"), str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
