@@ -898,12 +898,14 @@ def test_moe_layer_f32_vs_oracle(qm, orc, cfg):
     rl.close()
 
 
-@pytest.mark.parametrize("T", [1, 5, 16])
+@pytest.mark.parametrize("T", [1, 5, 16, 512])
 def test_moe_ffn_host_equals_device(qm, orc, T):
     """qmag_moe_ffn_host (x and out in host memory, the engine's moe_ffn call)
     gives the bits of qmag_moe_ffn_dev on the same input: the persistent
     one-layer kernel (T = 1), the launch sequence (T = 5) and the grouped
-    prefill (T = 16), the stage buffers those of the same path."""
+    prefill (T = 16, and T = 512, the C5 batch, after the smaller calls: the
+    pinned staging grows from one to 512 rows), the stage buffers those of
+    the same path."""
     rl = qm.ResidentLayer(seed=7, layer=1)
     x = orc.fill_normal(90 + T, T * 2048, 0.0, 1.0)
     want = run_layer(qm, rl, x, T).reshape(-1)
